@@ -1,0 +1,177 @@
+"""CARL step-engine benchmark on one MI355X.
+
+Workload (headline): 1v1, fp32, n_sim = 65536, tick_skip = 8; even arenas
+start from kickoff, odd arenas from seeded random states; seeded random
+continuous actions (a pool of 64 action batches cycled per step); every env
+step runs the full native sequence - 8 physics ticks, rewards/dones,
+transition state/obs, done resets, obs/state packing - plus the default score
+reward (score delta x team sign).  Inputs are resident in HBM before timing.
+
+Prints one JSON line:
+  value          sim-ticks/s = n_sim * tick_skip * steps / seconds
+  roofline       the fused tick kernel: algorithmic bytes (1,488 B per 1v1
+                 sim-tick: persistent state read + written + actions) per
+                 launch / average launch time from HIP events on the engine
+                 stream, against 8 TB/s
+  cpu_baseline   the CPU model of the same physics (oracle/liboracle.so), one
+                 1v1 arena per thread on this host's cores, direct controls
+                 held 8 ticks (bounded sample)
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+METRIC = "sim-ticks/sec (n_sim×ticks) 1v1 n_sim=65536 on 1 GPU; % HBM roofline"
+HBM_PEAK_GBS = 8000.0
+BYTES_PER_CAR = 232      # persistent per-car state carried across ticks
+BYTES_PER_SIM = 252      # persistent per-simulation state
+ACTION_BYTES = 28        # one car's action per tick
+
+
+def tick_bytes(n_cars: int) -> int:
+    """Algorithmic HBM bytes of one simulation tick (state read + write + actions)."""
+    return 2 * (n_cars * BYTES_PER_CAR + BYTES_PER_SIM) + n_cars * ACTION_BYTES
+
+
+def cpu_baseline(ticks_per_thread: int, seed: int) -> dict:
+    import ctypes
+
+    lib_path = ROOT / "oracle" / "liboracle.so"
+    lib = ctypes.CDLL(str(lib_path))
+    lib.oracle_cpu_throughput.restype = ctypes.c_double
+    lib.oracle_cpu_throughput.argtypes = [ctypes.c_char_p, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+    cores = len(os.sched_getaffinity(0))
+    obj = str(ROOT / "carl_amd" / "assets" / "arena.obj").encode()
+    rate = lib.oracle_cpu_throughput(obj, cores, ticks_per_thread, seed)
+    return {
+        "value": rate,
+        "unit": "sim-ticks/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"1v1 arena per thread x {cores} threads, {ticks_per_thread} ticks each, seeded direct "
+                   f"controls held 8 ticks, done-resets every tick (CPU model of the same physics)"),
+    }
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--n-sim", type=int, default=65536)
+    ap.add_argument("--blue", type=int, default=1)
+    ap.add_argument("--orange", type=int, default=1)
+    ap.add_argument("--tick-skip", type=int, default=8)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--cpu-ticks", type=int, default=1_200_000,
+                    help="CPU-baseline ticks per host thread (0 skips it)")
+    ap.add_argument("--kernel-launches", type=int, default=100)
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
+              "(simulations shard across GPUs with no exchange; see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import carl_amd
+    from carl_amd import workloads
+
+    dev = torch.device("cuda:0")
+    n_sim, n_cars = args.n_sim, args.blue + args.orange
+    rng = np.random.default_rng(args.seed)
+    env = carl_amd.Env(n_sim, args.blue, args.orange, args.seed, args.tick_skip, True, False, False)
+    stream = torch.cuda.ExternalStream(env.stream, device=dev)
+
+    odd = np.arange(1, n_sim, 2)
+    reset = workloads.random_reset_state(rng, len(odd), n_cars)
+    env.apply_reset_state(**{k: torch.from_numpy(v).to(dev) for k, v in reset.items()},
+                          simulation_indices=torch.from_numpy(odd.astype(np.int64)).to(dev))
+    pool = [torch.from_numpy(workloads.random_continuous_actions(rng, n_sim, n_cars)).to(dev) for _ in range(64)]
+    team_sign = torch.tensor([1.0] * args.blue + [-1.0] * args.orange, device=dev)
+    torch.cuda.synchronize()
+
+    def env_step(i: int) -> torch.Tensor:
+        env.step_continuous(pool[i % len(pool)])
+        with torch.cuda.stream(stream):
+            score = torch.from_dlpack(env.get_rewards())
+            return (score[:, None] * team_sign).reshape(-1)  # default score reward
+
+    for i in range(args.warmup):
+        env_step(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        reward = env_step(i)
+    torch.cuda.synchronize()
+    seconds = time.perf_counter() - t0
+    del reward
+
+    sim_ticks = n_sim * args.tick_skip * args.steps
+    value = sim_ticks / seconds
+
+    # dominant kernel: the fused tick kernel, one launch per frameskip window
+    launches = args.kernel_launches
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for i in range(3):
+        env.tick(pool[i], 1, args.tick_skip)
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        for i in range(launches):
+            env.tick(pool[i % len(pool)], 1, args.tick_skip)
+        stop.record(stream)
+    stop.synchronize()
+    launch_ms = start.elapsed_time(stop) / launches
+    launch_bytes = tick_bytes(n_cars) * n_sim * args.tick_skip
+    achieved = launch_bytes / (launch_ms * 1e-3) / 1e9
+
+    result = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "sim-ticks/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": seconds * 1e3 / args.steps,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "env_steps_per_s": n_sim * args.steps / seconds,
+        "config": {
+            "workload": (f"{args.blue}v{args.orange} n_sim={n_sim} tick_skip={args.tick_skip}: kickoff + seeded "
+                         "random states, seeded random continuous actions, obs/state packing, done resets, "
+                         "default score reward"),
+            "n_sim": n_sim,
+            "n_cars": n_cars,
+            "tick_skip": args.tick_skip,
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "tickKernel",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": None,
+            "launch_ms": launch_ms,
+            "bytes_per_launch": launch_bytes,
+        },
+    }
+    if args.cpu_ticks > 0:
+        result["cpu_baseline"] = cpu_baseline(args.cpu_ticks, args.seed)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,25 @@
+// arena.h - host-side construction of the soccar collision mesh.
+#pragma once
+
+#include <string>
+#include <vector>
+
+namespace carl {
+
+struct HostArena {
+    std::vector<float> verts;       // 3 per welded vertex
+    std::vector<int> tris;          // 3 per triangle
+    std::vector<float> normals;     // 3 per triangle
+    std::vector<float> angles;      // 3 per triangle (signed edge angles)
+    std::vector<int> cellStart;     // kCells + 1
+    std::vector<int> cellTris;      // triangle per cell reference, ascending within a cell
+    std::vector<float> records;     // 16 floats per cell reference (device layout, see state.h)
+};
+
+// Parse, weld and index the mesh.  Returns "" on success, else the error text.
+std::string buildArena(const std::string& objPath, HostArena& out);
+
+// Locate arena.obj: $CARL_ARENA_OBJ, then assets/arena.obj next to the package.
+std::string findArenaObj(const std::string& libraryDir);
+
+}  // namespace carl

@@ -1,0 +1,788 @@
+// engine.hip - kernels, host engine and C-ABI of the MI355X CARL step engine.
+//
+// Tick pipeline: one launch runs a whole frameskip window.  A workgroup owns
+// a tile of whole simulations (lanes = cars), so the reference's eleven
+// per-tick launches (src/RLEnvironment.cu:166-211) become phases separated by
+// workgroup barriers:
+//   A1  per car: broadphase + suspension raycast   (reads other cars' poses)
+//   A2  per car: controls, car-arena SAT/clip/manifold, suspension + solve
+//   B   per sim: episode tick, car-car pairs, ball arena + car-ball + goal
+//   C   per car: integrate + impulse cache / demo respawn; per sim: ball finish
+//   D   per sim: boost pads
+// State stays in the structure-of-arrays planes (L2 / MALL resident between
+// phases); no per-tick workspace buffers exist.
+#include <dlfcn.h>
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <array>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/carl_amd.h"
+#include "arena.h"
+#include "envio.h"
+
+using namespace carl;
+
+namespace {
+
+thread_local std::string g_lastError;
+
+int fail(int code, const std::string& msg)
+{
+    g_lastError = msg;
+    return code;
+}
+
+#define HIP_TRY(expr)                                                                   \
+    do {                                                                                \
+        hipError_t e_ = (expr);                                                         \
+        if (e_ != hipSuccess)                                                           \
+            return fail(CARL_ERR_RUNTIME, std::string(#expr) + ": " + hipGetErrorString(e_)); \
+    } while (0)
+
+// ------------------------------------------------------------------ kernels
+
+constexpr int kTickBlock = 256;
+
+__global__ __launch_bounds__(kTickBlock) void tickKernel(Dev d, int nOrange, int tick0, int nTicks, int kind,
+                                                         const void* __restrict__ actions, int simsPerBlock)
+{
+    const int t = threadIdx.x;
+    const int simBase = blockIdx.x * simsPerBlock;
+    const int mySim = simBase + t / d.nCars;
+    const bool carOk = t < simsPerBlock * d.nCars && mySim < d.nSim;
+    const int car = mySim * d.nCars + t % d.nCars;
+    const int laneSim = simBase + t;
+    const bool simOk = t < simsPerBlock && laneSim < d.nSim;
+    Controls ctl{};
+    if (carOk) ctl = decodeControls(kind, actions, car);
+
+    for (int k = 0; k < nTicks; k++) {
+        const int tick = tick0 + k + 1;
+        Wheels w;
+        Broad bp{ 0, 0 };
+        if (carOk) {
+            const V3 cen = d.cv(CARL_CAR_CEN, car);
+            const Q4 rot = d.cq(CARL_CAR_ROT, car);
+            bp = broadphase(d, d.cv(CARL_CAR_POS, car), d.cv(CARL_CAR_VEL, car), d.cv(CARL_CAR_ANG, car), cen, rot);
+            raycast(d, car, mySim, cen, rot, bp, w);
+        }
+        __syncthreads();
+        if (carOk) {
+            storeWheelOutputs(d, car, w);
+            d.setf(CARL_CAR_CTRL_THROTTLE, car, ctl.throttle);
+            d.setf(CARL_CAR_CTRL_STEER, car, ctl.steer);
+            d.setf(CARL_CAR_CTRL_YAW, car, ctl.yaw);
+            d.setf(CARL_CAR_CTRL_PITCH, car, ctl.pitch);
+            d.setf(CARL_CAR_CTRL_ROLL, car, ctl.roll);
+            d.seti(CARL_CAR_CTRL_JUMP, car, ctl.jump);
+            d.seti(CARL_CAR_CTRL_BOOST, car, ctl.boost);
+            d.seti(CARL_CAR_CTRL_SLIDE, car, ctl.slide);
+            if (!d.ci(CARL_CAR_DEMOED, car)) {
+                CarRegs r;
+                loadRegs(d, car, r);
+                applyControls(r, ctl, w);
+                solveCarArena(d, r, w, bp, tick);
+                storeRegs(d, car, r);
+            }
+        }
+        __syncthreads();
+        if (simOk) {
+            d.sseti(CARL_SIM_EPISODE_TICKS, laneSim, d.si(CARL_SIM_EPISODE_TICKS, laneSim) + 1);
+            const int base = laneSim * d.nCars;
+            for (int a = 0; a < d.nCars - 1; a++)
+                for (int b = a + 1; b < d.nCars; b++) carCarPair(d, base + b, base + a, tick);
+            ballTick(d, laneSim, tick);
+        }
+        __syncthreads();
+        if (carOk) finishCar(d, car);
+        if (simOk) finishBall(d, laneSim);
+        __syncthreads();
+        if (simOk) boostPads(d, laneSim);
+        __syncthreads();
+    }
+}
+
+__global__ void resetKernel(Dev d, int nOrange)
+{
+    const int s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s < d.nSim) fullResetSim(d, s, nOrange);
+}
+
+__global__ void resetDonesKernel(Dev d, int nOrange, int tickCount, DoneRule rule)
+{
+    const int s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s < d.nSim) resetAfterDone(d, s, tickCount, rule, nOrange);
+}
+
+__global__ void rewardsDonesKernel(Dev d, int tickCount, DoneRule rule, float* rewards, bool* dones, int* tScore,
+                                   int* tTicks, bool* tOvertime)
+{
+    const int s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s >= d.nSim) return;
+    rewards[s] = (float)d.si(CARL_SIM_LAST_SCORER, s);
+    dones[s] = simDone(d, s, tickCount, rule);
+    tScore[s] = d.si(CARL_SIM_BLUE_SCORE, s) - d.si(CARL_SIM_ORANGE_SCORE, s);
+    tTicks[s] = d.si(CARL_SIM_EPISODE_TICKS, s);
+    tOvertime[s] = d.si(CARL_SIM_OVERTIME, s) != 0;
+}
+
+__global__ void matchKernel(Dev d, int* score, int* ticks, bool* overtime, const bool* mask)
+{
+    const int s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s >= d.nSim || (mask && !mask[s])) return;
+    score[s] = d.si(CARL_SIM_BLUE_SCORE, s) - d.si(CARL_SIM_ORANGE_SCORE, s);
+    ticks[s] = d.si(CARL_SIM_EPISODE_TICKS, s);
+    overtime[s] = d.si(CARL_SIM_OVERTIME, s) != 0;
+}
+
+__global__ void stateKernel(Dev d, float* out, int stateDimV, int touchWindow, int tickCount, const bool* mask)
+{
+    const int s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s >= d.nSim || (mask && !mask[s])) return;
+    packStateRow(d, s, touchWindow, tickCount, out + (size_t)s * stateDimV);
+}
+
+__global__ void obsKernel(Dev d, float* out, int obsDimV, const bool* mask, int invert, int normalizeObs, int prev)
+{
+    const int a = blockIdx.x * blockDim.x + threadIdx.x;
+    if (a >= d.nTotal) return;
+    const int s = a / d.nCars;
+    if (mask && !mask[s]) return;
+    packObservation(d, s, a % d.nCars, invert != 0, normalizeObs != 0, prev != 0, out + (size_t)a * obsDimV);
+}
+
+__global__ void setBallKernel(Dev d, const float* pos, const float* vel, const float* ang, Selection sel)
+{
+    const int r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= sel.n) return;
+    const int t = selectRow(sel, r, d.nSim);
+    if (t < 0) return;
+    d.ssetv(CARL_SIM_BALL_POS, t, V3{ pos[3 * r], pos[3 * r + 1], pos[3 * r + 2] });
+    d.ssetv(CARL_SIM_BALL_VEL, t, V3{ vel[3 * r], vel[3 * r + 1], vel[3 * r + 2] });
+    d.ssetv(CARL_SIM_BALL_ANG, t, V3{ ang[3 * r], ang[3 * r + 1], ang[3 * r + 2] });
+    d.ssetv(CARL_SIM_BALL_IMP, t, kZero);
+}
+
+__global__ void setCarKernel(Dev d, const float* pos, const float* rot, const float* vel, const float* ang,
+                             const void* demoed, int byteDemoed, const float* boost, const float* internal,
+                             Selection sel)
+{
+    const int src = blockIdx.x * blockDim.x + threadIdx.x;
+    if (src >= sel.n * d.nCars) return;
+    const int t = selectRow(sel, src / d.nCars, d.nSim);
+    if (t < 0) return;
+    setCarRow(d, src, t, src % d.nCars, pos, rot, vel, ang, demoed, byteDemoed != 0, boost, internal);
+}
+
+__global__ void refreshKernel(Dev d, Selection sel)
+{
+    const int src = blockIdx.x * blockDim.x + threadIdx.x;
+    if (src >= sel.n * d.nCars) return;
+    const int t = selectRow(sel, src / d.nCars, d.nSim);
+    if (t < 0) return;
+    refreshContacts(d, t * d.nCars + src % d.nCars);
+}
+
+__global__ void setMatchKernel(Dev d, const int32_t* blue, const int32_t* orange, const int32_t* ticks, Selection sel)
+{
+    const int r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= sel.n) return;
+    const int t = selectRow(sel, r, d.nSim);
+    if (t < 0) return;
+    d.sseti(CARL_SIM_BLUE_SCORE, t, blue[r]);
+    d.sseti(CARL_SIM_ORANGE_SCORE, t, orange[r]);
+    d.sseti(CARL_SIM_LAST_SCORER, t, 0);
+    d.sseti(CARL_SIM_OVERTIME, t, 0);
+    d.sseti(CARL_SIM_EPISODE_TICKS, t, ticks[r]);
+}
+
+__global__ void resetPadsKernel(Dev d, Selection sel)
+{
+    const int r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= sel.n) return;
+    const int t = selectRow(sel, r, d.nSim);
+    if (t < 0) return;
+    for (int p = 0; p < kPads; p++) d.ssetf(CARL_SIM_PAD_COOLDOWN + p, t, 0.f);
+}
+
+// ---- wave64 DPP inclusive scan (no library): Hillis-Steele inside each row
+// of 16 lanes with row_shr 1/2/4/8, then row_bcast:15 and row_bcast:31 carry
+// the row totals across the four rows.
+__device__ __forceinline__ int waveInclusiveScan(int v)
+{
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15 -> rows 1,3
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31 -> rows 2,3
+    return v;
+}
+
+constexpr int kScanBlock = 256;
+constexpr int kScanItems = 8;
+constexpr int kScanTile = kScanBlock * kScanItems;
+
+// exclusive scan of one tile per block; block totals to `sums` when given
+__global__ __launch_bounds__(kScanBlock) void scanTileKernel(const int32_t* in, int32_t* out, int n, int32_t* sums)
+{
+    __shared__ int waveTotals[kScanBlock / 64];
+    const int base = blockIdx.x * kScanTile + threadIdx.x * kScanItems;
+    int v[kScanItems];
+    int local = 0;
+#pragma unroll
+    for (int i = 0; i < kScanItems; i++) {
+        v[i] = base + i < n ? in[base + i] : 0;
+        local += v[i];
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int incl = waveInclusiveScan(local);
+    if (lane == 63) waveTotals[wave] = incl;
+    __syncthreads();
+    int waveOffset = 0;
+    for (int w = 0; w < wave; w++) waveOffset += waveTotals[w];
+    int run = waveOffset + incl - local;
+#pragma unroll
+    for (int i = 0; i < kScanItems; i++) {
+        if (base + i < n) out[base + i] = run;
+        run += v[i];
+    }
+    if (sums && threadIdx.x == kScanBlock - 1) sums[blockIdx.x] = waveOffset + incl;
+}
+
+__global__ void scanAddKernel(int32_t* out, int n, const int32_t* offsets)
+{
+    const int i = blockIdx.x * kScanTile + threadIdx.x;
+    for (int k = 0; k < kScanItems; k++) {
+        const int idx = i + k * kScanBlock;
+        if (idx < n) out[idx] += offsets[blockIdx.x];
+    }
+}
+
+int runScan(const int32_t* in, int32_t* out, int n, hipStream_t stream)
+{
+    if (n <= 0) return CARL_OK;
+    const int tiles = (n + kScanTile - 1) / kScanTile;
+    if (tiles == 1) {
+        scanTileKernel<<<1, kScanBlock, 0, stream>>>(in, out, n, nullptr);
+        HIP_TRY(hipGetLastError());
+        return CARL_OK;
+    }
+    int32_t* sums = nullptr;
+    HIP_TRY(hipMallocAsync((void**)&sums, sizeof(int32_t) * 2 * tiles, stream));
+    scanTileKernel<<<tiles, kScanBlock, 0, stream>>>(in, out, n, sums);
+    HIP_TRY(hipGetLastError());
+    const int rc = runScan(sums, sums + tiles, tiles, stream);
+    if (rc != CARL_OK) return rc;
+    scanAddKernel<<<tiles, kScanBlock, 0, stream>>>(out, n, sums + tiles);
+    HIP_TRY(hipGetLastError());
+    HIP_TRY(hipFreeAsync(sums, stream));
+    return CARL_OK;
+}
+
+std::string libraryDir()
+{
+    Dl_info info{};
+    if (dladdr((void*)&libraryDir, &info) && info.dli_fname) {
+        std::string p = info.dli_fname;
+        const size_t slash = p.rfind('/');
+        if (slash != std::string::npos) return p.substr(0, slash);
+    }
+    return ".";
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------- engine
+
+struct carl_env {
+    int nSim = 0, nBlue = 0, nOrange = 0, nCars = 0, nTotal = 0, seed = 0;
+    int frameskip = 1;
+    bool invert = true, normalize = false, prevControls = false;
+    int obsDim = 0, stateDim = 0;
+    int maxTicks = kRegulationTicks, overtimeTicks = kRegulationTicks, noTouchTicks = 0;
+    int tickCount = 0;
+    hipStream_t stream = nullptr;
+    uint32_t* car = nullptr;
+    uint32_t* sim = nullptr;
+    float4* rec = nullptr;
+    int* cellStart = nullptr;
+    float4* angles = nullptr;
+    float *obs = nullptr, *tobs = nullptr, *state = nullptr, *tstate = nullptr, *rewards = nullptr;
+    bool *dones = nullptr, *overtime = nullptr, *tovertime = nullptr;
+    int32_t *score = nullptr, *ticks = nullptr, *tscore = nullptr, *tticks = nullptr;
+    int32_t* actions = nullptr;
+    float* cactions = nullptr;
+
+    Dev dev() const
+    {
+        Dev d;
+        d.car = car; d.sim = sim; d.nSim = nSim; d.nBlue = nBlue; d.nCars = nCars; d.nTotal = nTotal; d.seed = seed;
+        d.arena = ArenaView{ rec, cellStart, angles };
+        return d;
+    }
+    DoneRule rule() const { return DoneRule{ maxTicks, overtimeTicks, noTouchTicks }; }
+    int grid(int n, int block) const { return (n + block - 1) / block; }
+};
+
+namespace {
+
+template <typename T>
+int devAlloc(T** p, size_t count)
+{
+    HIP_TRY(hipMalloc((void**)p, std::max<size_t>(count, 1) * sizeof(T)));
+    HIP_TRY(hipMemset(*p, 0, std::max<size_t>(count, 1) * sizeof(T)));
+    return CARL_OK;
+}
+
+void freeAll(carl_env* e)
+{
+    void* ptrs[] = { e->car, e->sim, e->rec, e->cellStart, e->angles, e->obs, e->tobs, e->state, e->tstate,
+                     e->rewards, e->dones, e->overtime, e->tovertime, e->score, e->ticks, e->tscore, e->tticks,
+                     e->actions, e->cactions };
+    for (void* p : ptrs)
+        if (p) (void)hipFree(p);
+    if (e->stream) (void)hipStreamDestroy(e->stream);
+}
+
+int launchTicks(carl_env* e, int kind, const void* actions, int n)
+{
+    if (n <= 0) return CARL_OK;
+    const int spb = kTickBlock / e->nCars;
+    const int blocks = (e->nSim + spb - 1) / spb;
+    tickKernel<<<blocks, spb * e->nCars, 0, e->stream>>>(e->dev(), e->nOrange, e->tickCount, n, kind, actions, spb);
+    HIP_TRY(hipGetLastError());
+    e->tickCount += n;
+    return CARL_OK;
+}
+
+int packObs(carl_env* e, float* out, const bool* mask)
+{
+    obsKernel<<<e->grid(e->nTotal, 128), 128, 0, e->stream>>>(e->dev(), out, e->obsDim, mask, e->invert, e->normalize,
+                                                              e->prevControls);
+    HIP_TRY(hipGetLastError());
+    return CARL_OK;
+}
+
+int packState(carl_env* e, float* out, int touchWindow, const bool* mask)
+{
+    stateKernel<<<e->grid(e->nSim, 64), 64, 0, e->stream>>>(e->dev(), out, e->stateDim, touchWindow, e->tickCount,
+                                                            mask);
+    HIP_TRY(hipGetLastError());
+    return CARL_OK;
+}
+
+int packMatch(carl_env* e, const bool* mask)
+{
+    matchKernel<<<e->grid(e->nSim, 64), 64, 0, e->stream>>>(e->dev(), e->score, e->ticks, e->overtime, mask);
+    HIP_TRY(hipGetLastError());
+    return CARL_OK;
+}
+
+int packRewardsDones(carl_env* e)
+{
+    rewardsDonesKernel<<<e->grid(e->nSim, 64), 64, 0, e->stream>>>(e->dev(), e->tickCount, e->rule(), e->rewards,
+                                                                   e->dones, e->tscore, e->tticks, e->tovertime);
+    HIP_TRY(hipGetLastError());
+    return CARL_OK;
+}
+
+#define CARL_TRY(expr)                 \
+    do {                               \
+        const int rc_ = (expr);        \
+        if (rc_ != CARL_OK) return rc_; \
+    } while (0)
+
+int initialPacks(carl_env* e)
+{
+    CARL_TRY(packObs(e, e->obs, nullptr));
+    CARL_TRY(packState(e, e->state, 1, nullptr));
+    CARL_TRY(packState(e, e->tstate, 1, nullptr));
+    CARL_TRY(packRewardsDones(e));
+    CARL_TRY(packMatch(e, nullptr));
+    return CARL_OK;
+}
+
+int fullReset(carl_env* e)
+{
+    e->tickCount = 0;
+    resetKernel<<<e->grid(e->nSim, 64), 64, 0, e->stream>>>(e->dev(), e->nOrange);
+    HIP_TRY(hipGetLastError());
+    return initialPacks(e);
+}
+
+Selection makeSel(const int64_t* idx, const uint8_t* mask, int n) { return Selection{ idx, mask, n }; }
+
+int setBallRows(carl_env* e, const float* pos, const float* vel, const float* ang, Selection sel)
+{
+    if (sel.n == 0) return CARL_OK;
+    setBallKernel<<<e->grid(sel.n, 64), 64, 0, e->stream>>>(e->dev(), pos, vel, ang, sel);
+    HIP_TRY(hipGetLastError());
+    return CARL_OK;
+}
+
+int setCarRows(carl_env* e, const float* pos, const float* rot, const float* vel, const float* ang, const void* demoed,
+               int byteDemoed, const float* boost, const float* internal, Selection sel)
+{
+    if (sel.n == 0) return CARL_OK;
+    const int n = sel.n * e->nCars;
+    setCarKernel<<<e->grid(n, 256), 256, 0, e->stream>>>(e->dev(), pos, rot, vel, ang, demoed, byteDemoed, boost,
+                                                          internal, sel);
+    HIP_TRY(hipGetLastError());
+    refreshKernel<<<e->grid(n, 256), 256, 0, e->stream>>>(e->dev(), sel);
+    HIP_TRY(hipGetLastError());
+    return CARL_OK;
+}
+
+int setMatchRows(carl_env* e, const int32_t* blue, const int32_t* orange, const int32_t* ticks, Selection sel)
+{
+    if (sel.n == 0) return CARL_OK;
+    setMatchKernel<<<e->grid(sel.n, 64), 64, 0, e->stream>>>(e->dev(), blue, orange, ticks, sel);
+    HIP_TRY(hipGetLastError());
+    return CARL_OK;
+}
+
+int resetPadRows(carl_env* e, Selection sel)
+{
+    if (sel.n == 0) return CARL_OK;
+    resetPadsKernel<<<e->grid(sel.n, 64), 64, 0, e->stream>>>(e->dev(), sel);
+    HIP_TRY(hipGetLastError());
+    return CARL_OK;
+}
+
+int checkEnv(carl_env* e)
+{
+    if (!e) return fail(CARL_ERR_VALUE, "null environment handle");
+    return CARL_OK;
+}
+
+int checkSelection(carl_env* e, int n)
+{
+    if (n < 0 || n > e->nSim) return fail(CARL_ERR_VALUE, "too many simulation_indices");
+    return CARL_OK;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------- C-ABI
+
+extern "C" {
+
+const char* carl_last_error(void) { return g_lastError.c_str(); }
+
+int carl_observation_dim(int nCars, int prev) { return observationDim(nCars, prev != 0); }
+int carl_state_dim(int nCars) { return stateDim(nCars); }
+
+int carl_env_create(int nSim, int nBlue, int nOrange, int seed, int frameskip, int flags, carl_env** out)
+{
+    if (!out) return fail(CARL_ERR_VALUE, "null output handle");
+    *out = nullptr;
+    if (frameskip < 1) return fail(CARL_ERR_VALUE, "frameskip must be at least 1");
+    if (nSim < 1) return fail(CARL_ERR_VALUE, "n_sim must be at least 1");
+    if (nBlue < 0 || nOrange < 0 || nBlue + nOrange < 1) return fail(CARL_ERR_VALUE, "need at least one car");
+    if (nBlue > 4 || nOrange > 4) return fail(CARL_ERR_VALUE, "at most 4 cars per team (kickoff spawns)");
+
+    carl::HostArena host;
+    const std::string path = findArenaObj(libraryDir());
+    const std::string err = buildArena(path, host);
+    if (!err.empty()) return fail(CARL_ERR_ARENA, err);
+
+    carl_env* e = new carl_env();
+    e->nSim = nSim; e->nBlue = nBlue; e->nOrange = nOrange; e->nCars = nBlue + nOrange;
+    e->nTotal = nSim * e->nCars; e->seed = seed; e->frameskip = frameskip;
+    e->invert = (flags & CARL_FLAG_INVERT_ORANGE) != 0;
+    e->normalize = (flags & CARL_FLAG_NORMALIZE) != 0;
+    e->prevControls = (flags & CARL_FLAG_PREVIOUS_CONTROLS) != 0;
+    e->obsDim = observationDim(e->nCars, e->prevControls);
+    e->stateDim = stateDim(e->nCars);
+
+    auto bail = [&](int rc) {
+        freeAll(e);
+        delete e;
+        return rc;
+    };
+    if (hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking) != hipSuccess)
+        return bail(fail(CARL_ERR_RUNTIME, "hipStreamCreate failed"));
+    const size_t nT = (size_t)e->nTotal, nS = (size_t)nSim;
+    int rc = CARL_OK;
+    rc = rc ? rc : devAlloc(&e->car, (size_t)CARL_CAR_FIELDS * nT);
+    rc = rc ? rc : devAlloc(&e->sim, (size_t)CARL_SIM_FIELDS * nS);
+    rc = rc ? rc : devAlloc(&e->rec, host.records.size() / 4);
+    rc = rc ? rc : devAlloc(&e->cellStart, host.cellStart.size());
+    rc = rc ? rc : devAlloc(&e->angles, host.angles.size() / 3);
+    rc = rc ? rc : devAlloc(&e->obs, nT * e->obsDim);
+    rc = rc ? rc : devAlloc(&e->tobs, nT * e->obsDim);
+    rc = rc ? rc : devAlloc(&e->state, nS * e->stateDim);
+    rc = rc ? rc : devAlloc(&e->tstate, nS * e->stateDim);
+    rc = rc ? rc : devAlloc(&e->rewards, nS);
+    rc = rc ? rc : devAlloc(&e->dones, nS);
+    rc = rc ? rc : devAlloc(&e->overtime, nS);
+    rc = rc ? rc : devAlloc(&e->tovertime, nS);
+    rc = rc ? rc : devAlloc(&e->score, nS);
+    rc = rc ? rc : devAlloc(&e->ticks, nS);
+    rc = rc ? rc : devAlloc(&e->tscore, nS);
+    rc = rc ? rc : devAlloc(&e->tticks, nS);
+    rc = rc ? rc : devAlloc(&e->actions, nT * 7);
+    rc = rc ? rc : devAlloc(&e->cactions, nT * 7);
+    if (rc) return bail(rc);
+
+    std::vector<float4> ang(host.angles.size() / 3);
+    for (size_t t = 0; t < ang.size(); t++)
+        ang[t] = make_float4(host.angles[3 * t], host.angles[3 * t + 1], host.angles[3 * t + 2], 0.f);
+    if (hipMemcpy(e->rec, host.records.data(), host.records.size() * sizeof(float), hipMemcpyHostToDevice) != hipSuccess
+        || hipMemcpy(e->cellStart, host.cellStart.data(), host.cellStart.size() * sizeof(int), hipMemcpyHostToDevice)
+               != hipSuccess
+        || hipMemcpy(e->angles, ang.data(), ang.size() * sizeof(float4), hipMemcpyHostToDevice) != hipSuccess)
+        return bail(fail(CARL_ERR_RUNTIME, "arena upload failed"));
+
+    rc = fullReset(e);
+    if (rc) return bail(rc);
+    *out = e;
+    return CARL_OK;
+}
+
+int carl_env_destroy(carl_env* e)
+{
+    if (!e) return CARL_OK;
+    if (e->stream) (void)hipStreamSynchronize(e->stream);
+    freeAll(e);
+    delete e;
+    return CARL_OK;
+}
+
+void* carl_env_stream(carl_env* e) { return e ? (void*)e->stream : nullptr; }
+
+int carl_env_synchronize(carl_env* e)
+{
+    CARL_TRY(checkEnv(e));
+    HIP_TRY(hipStreamSynchronize(e->stream));
+    return CARL_OK;
+}
+
+int carl_env_tick(carl_env* e, int kind, const void* actions, int n)
+{
+    CARL_TRY(checkEnv(e));
+    if (kind < CARL_ACTIONS_DISCRETE || kind > CARL_ACTIONS_DIRECT) return fail(CARL_ERR_VALUE, "unknown action kind");
+    if (!actions) return fail(CARL_ERR_VALUE, "null actions");
+    return launchTicks(e, kind, actions, n);
+}
+
+int carl_env_reset_dones(carl_env* e)
+{
+    CARL_TRY(checkEnv(e));
+    resetDonesKernel<<<e->grid(e->nSim, 64), 64, 0, e->stream>>>(e->dev(), e->nOrange, e->tickCount, e->rule());
+    HIP_TRY(hipGetLastError());
+    return CARL_OK;
+}
+
+int carl_env_step(carl_env* e, int kind, const void* actions)
+{
+    CARL_TRY(checkEnv(e));
+    if (!actions) return fail(CARL_ERR_VALUE, "null actions");
+    const void* src = actions;
+    const size_t bytes = (size_t)e->nTotal * 7 * 4;
+    if (kind == CARL_ACTIONS_DISCRETE) {
+        HIP_TRY(hipMemcpyAsync(e->actions, actions, bytes, hipMemcpyDeviceToDevice, e->stream));
+        src = e->actions;
+    } else if (kind == CARL_ACTIONS_CONTINUOUS) {
+        HIP_TRY(hipMemcpyAsync(e->cactions, actions, bytes, hipMemcpyDeviceToDevice, e->stream));
+        src = e->cactions;
+    } else if (kind != CARL_ACTIONS_DIRECT) {
+        return fail(CARL_ERR_VALUE, "unknown action kind");
+    }
+    CARL_TRY(launchTicks(e, kind, src, e->frameskip));
+    CARL_TRY(packRewardsDones(e));
+    CARL_TRY(packState(e, e->tstate, e->frameskip, nullptr));
+    CARL_TRY(packObs(e, e->tobs, e->dones));
+    CARL_TRY(carl_env_reset_dones(e));
+    CARL_TRY(packMatch(e, nullptr));
+    CARL_TRY(packObs(e, e->obs, nullptr));
+    CARL_TRY(packState(e, e->state, 1, nullptr));
+    return CARL_OK;
+}
+
+int carl_env_reset(carl_env* e)
+{
+    CARL_TRY(checkEnv(e));
+    return fullReset(e);
+}
+
+int carl_env_set_ball(carl_env* e, const float* pos, const float* vel, const float* ang, const int64_t* idx, int n)
+{
+    CARL_TRY(checkEnv(e));
+    if (!idx) n = e->nSim;
+    CARL_TRY(checkSelection(e, n));
+    if (n > 0 && (!pos || !vel || !ang)) return fail(CARL_ERR_VALUE, "null ball input");
+    CARL_TRY(setBallRows(e, pos, vel, ang, makeSel(idx, nullptr, n)));
+    CARL_TRY(packObs(e, e->obs, nullptr));
+    CARL_TRY(packState(e, e->state, 1, nullptr));
+    CARL_TRY(packState(e, e->tstate, 1, nullptr));
+    return CARL_OK;
+}
+
+int carl_env_set_car(carl_env* e, const float* pos, const float* rot, const float* vel, const float* ang,
+                     const void* demoed, int byteDemoed, const float* boost, const float* internal, const int64_t* idx,
+                     int n)
+{
+    CARL_TRY(checkEnv(e));
+    if (!idx) n = e->nSim;
+    CARL_TRY(checkSelection(e, n));
+    if (n > 0 && (!pos || !rot || !vel || !ang || !demoed)) return fail(CARL_ERR_VALUE, "null car input");
+    CARL_TRY(setCarRows(e, pos, rot, vel, ang, demoed, byteDemoed, boost, internal, makeSel(idx, nullptr, n)));
+    CARL_TRY(packObs(e, e->obs, nullptr));
+    CARL_TRY(packState(e, e->state, 1, nullptr));
+    CARL_TRY(packState(e, e->tstate, 1, nullptr));
+    return CARL_OK;
+}
+
+int carl_env_apply_reset(carl_env* e, const float* bpos, const float* bvel, const float* bang, const float* cpos,
+                         const float* crot, const float* cvel, const float* cang, const void* demoed, int byteDemoed,
+                         const float* boost, const float* internal, const int32_t* blue, const int32_t* orange,
+                         const int32_t* ticks, const int64_t* idx, int n, const uint8_t* mask)
+{
+    CARL_TRY(checkEnv(e));
+    if (idx && mask) return fail(CARL_ERR_VALUE, "specify reset_mask or simulation_indices, not both");
+    if (!idx) n = e->nSim;
+    CARL_TRY(checkSelection(e, n));
+    const bool hasMatch = blue != nullptr;
+    if (hasMatch != (orange != nullptr) || hasMatch != (ticks != nullptr))
+        return fail(CARL_ERR_VALUE, "blue_score, orange_score and episode_ticks must be supplied together");
+    if (n == 0) return CARL_OK;
+    if (!bpos || !bvel || !bang || !cpos || !crot || !cvel || !cang || !demoed)
+        return fail(CARL_ERR_VALUE, "null reset input");
+    const Selection sel = makeSel(idx, mask, n);
+    CARL_TRY(resetPadRows(e, sel));
+    CARL_TRY(setBallRows(e, bpos, bvel, bang, sel));
+    CARL_TRY(setCarRows(e, cpos, crot, cvel, cang, demoed, byteDemoed, boost, internal, sel));
+    if (hasMatch) CARL_TRY(setMatchRows(e, blue, orange, ticks, sel));
+    const bool* m = (const bool*)mask;
+    CARL_TRY(packObs(e, e->obs, m));
+    CARL_TRY(packState(e, e->state, 1, m));
+    CARL_TRY(packMatch(e, m));
+    return CARL_OK;
+}
+
+int carl_env_set_match(carl_env* e, const int32_t* blue, const int32_t* orange, const int32_t* ticks,
+                       const int64_t* idx, int n)
+{
+    CARL_TRY(checkEnv(e));
+    if (!idx) n = e->nSim;
+    CARL_TRY(checkSelection(e, n));
+    if (n > 0 && (!blue || !orange || !ticks)) return fail(CARL_ERR_VALUE, "null match input");
+    return setMatchRows(e, blue, orange, ticks, makeSel(idx, nullptr, n));
+}
+
+int carl_env_reset_pads(carl_env* e, const int64_t* idx, int n)
+{
+    CARL_TRY(checkEnv(e));
+    if (!idx) n = e->nSim;
+    CARL_TRY(checkSelection(e, n));
+    return resetPadRows(e, makeSel(idx, nullptr, n));
+}
+
+int carl_env_buffer(carl_env* e, int id, void** data, int64_t* shape, int* ndim, int* dtype)
+{
+    CARL_TRY(checkEnv(e));
+    if (!data || !shape || !ndim || !dtype) return fail(CARL_ERR_VALUE, "null output pointer");
+    const int64_t nS = e->nSim, nC = e->nCars;
+    auto set = [&](void* p, int nd, int64_t a, int64_t b, int64_t c, int dt) {
+        *data = p; *ndim = nd; shape[0] = a; shape[1] = b; shape[2] = c; *dtype = dt;
+        return CARL_OK;
+    };
+    switch (id) {
+    case CARL_BUF_OBS: return set(e->obs, 3, nS, nC, e->obsDim, CARL_DTYPE_F32);
+    case CARL_BUF_TRANSITION_OBS: return set(e->tobs, 3, nS, nC, e->obsDim, CARL_DTYPE_F32);
+    case CARL_BUF_STATE: return set(e->state, 2, nS, e->stateDim, 0, CARL_DTYPE_F32);
+    case CARL_BUF_TRANSITION_STATE: return set(e->tstate, 2, nS, e->stateDim, 0, CARL_DTYPE_F32);
+    case CARL_BUF_ACTIONS: return set(e->actions, 3, nS, nC, 7, CARL_DTYPE_I32);
+    case CARL_BUF_CONTINUOUS_ACTIONS: return set(e->cactions, 3, nS, nC, 7, CARL_DTYPE_F32);
+    case CARL_BUF_REWARDS: return set(e->rewards, 1, nS, 0, 0, CARL_DTYPE_F32);
+    case CARL_BUF_DONES: return set(e->dones, 1, nS, 0, 0, CARL_DTYPE_BOOL);
+    case CARL_BUF_SCORE_DIFFERENCE: return set(e->score, 1, nS, 0, 0, CARL_DTYPE_I32);
+    case CARL_BUF_EPISODE_TICKS: return set(e->ticks, 1, nS, 0, 0, CARL_DTYPE_I32);
+    case CARL_BUF_TRANSITION_SCORE_DIFFERENCE: return set(e->tscore, 1, nS, 0, 0, CARL_DTYPE_I32);
+    case CARL_BUF_TRANSITION_EPISODE_TICKS: return set(e->tticks, 1, nS, 0, 0, CARL_DTYPE_I32);
+    case CARL_BUF_OVERTIME: return set(e->overtime, 1, nS, 0, 0, CARL_DTYPE_BOOL);
+    case CARL_BUF_TRANSITION_OVERTIME: return set(e->tovertime, 1, nS, 0, 0, CARL_DTYPE_BOOL);
+    default: return fail(CARL_ERR_VALUE, "unknown buffer id");
+    }
+}
+
+int carl_env_set_param(carl_env* e, int p, int v)
+{
+    CARL_TRY(checkEnv(e));
+    switch (p) {
+    case CARL_PARAM_MAX_TICKS:
+        if (v < 1) return fail(CARL_ERR_VALUE, "max_ticks must be at least 1");
+        e->maxTicks = v;
+        return CARL_OK;
+    case CARL_PARAM_OVERTIME_TIMEOUT_TICKS:
+        if (v < 1) return fail(CARL_ERR_VALUE, "overtime_timeout_ticks must be at least 1");
+        e->overtimeTicks = v;
+        return CARL_OK;
+    case CARL_PARAM_NO_TOUCH_TIMEOUT_TICKS:
+        if (v < 0) return fail(CARL_ERR_VALUE, "no_touch_timeout_ticks must be non-negative");
+        e->noTouchTicks = v;
+        return CARL_OK;
+    case CARL_PARAM_FRAMESKIP:
+        if (v < 1) return fail(CARL_ERR_VALUE, "frameskip must be at least 1");
+        e->frameskip = v;
+        return CARL_OK;
+    default: return fail(CARL_ERR_VALUE, "parameter is read-only or unknown");
+    }
+}
+
+int carl_env_get_param(carl_env* e, int p, int* v)
+{
+    CARL_TRY(checkEnv(e));
+    if (!v) return fail(CARL_ERR_VALUE, "null output pointer");
+    switch (p) {
+    case CARL_PARAM_MAX_TICKS: *v = e->maxTicks; break;
+    case CARL_PARAM_OVERTIME_TIMEOUT_TICKS: *v = e->overtimeTicks; break;
+    case CARL_PARAM_NO_TOUCH_TIMEOUT_TICKS: *v = e->noTouchTicks; break;
+    case CARL_PARAM_FRAMESKIP: *v = e->frameskip; break;
+    case CARL_PARAM_N_SIM: *v = e->nSim; break;
+    case CARL_PARAM_N_CARS: *v = e->nCars; break;
+    case CARL_PARAM_OBS_DIM: *v = e->obsDim; break;
+    case CARL_PARAM_ACT_DIM: *v = e->nCars * 7; break;
+    case CARL_PARAM_STATE_DIM: *v = e->stateDim; break;
+    case CARL_PARAM_TICK_COUNT: *v = e->tickCount; break;
+    case CARL_PARAM_N_BLUE: *v = e->nBlue; break;
+    default: return fail(CARL_ERR_VALUE, "unknown parameter");
+    }
+    return CARL_OK;
+}
+
+int carl_env_export_state(carl_env* e, uint32_t* car, uint32_t* sim, int* tick)
+{
+    CARL_TRY(checkEnv(e));
+    HIP_TRY(hipStreamSynchronize(e->stream));
+    if (car) HIP_TRY(hipMemcpy(car, e->car, sizeof(uint32_t) * CARL_CAR_FIELDS * (size_t)e->nTotal, hipMemcpyDeviceToHost));
+    if (sim) HIP_TRY(hipMemcpy(sim, e->sim, sizeof(uint32_t) * CARL_SIM_FIELDS * (size_t)e->nSim, hipMemcpyDeviceToHost));
+    if (tick) *tick = e->tickCount;
+    return CARL_OK;
+}
+
+int carl_env_import_state(carl_env* e, const uint32_t* car, const uint32_t* sim, int tick)
+{
+    CARL_TRY(checkEnv(e));
+    if (!car || !sim) return fail(CARL_ERR_VALUE, "null state buffer");
+    HIP_TRY(hipStreamSynchronize(e->stream));
+    HIP_TRY(hipMemcpy(e->car, car, sizeof(uint32_t) * CARL_CAR_FIELDS * (size_t)e->nTotal, hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy(e->sim, sim, sizeof(uint32_t) * CARL_SIM_FIELDS * (size_t)e->nSim, hipMemcpyHostToDevice));
+    e->tickCount = tick;
+    return CARL_OK;
+}
+
+int carl_exclusive_scan_i32(const int32_t* in, int32_t* out, int n, void* stream)
+{
+    if (n < 0) return fail(CARL_ERR_VALUE, "negative length");
+    if (n > 0 && (!in || !out)) return fail(CARL_ERR_VALUE, "null scan buffer");
+    return runScan(in, out, n, (hipStream_t)stream);
+}
+
+}  // extern "C"

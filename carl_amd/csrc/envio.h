@@ -1,0 +1,373 @@
+// envio.h - observation / state / reward packing, resets and state setters.
+//
+// Reference semantics:
+//   observation layout and orange mirroring   include/Physics/Observations.cuh:9-238
+//   normalisation                             include/Physics/Observations.cuh:240-317
+//   canonical state                           include/Physics/Observations.cuh:320-356
+//   rewards, dones, overtime                  include/Physics/Observations.cuh:360-397
+//   kickoff / done resets                     include/State/Reset.cuh:8-171
+//   full reset                                include/State/GameState.cuh:221-231,
+//                                             include/State/Workspace.cuh:225-233
+//   setters and contact refresh               src/EnvIO.cu:137-357, 603-643
+#pragma once
+
+#include "sim_phase.h"
+
+namespace carl {
+
+DI V3 mirrorXY(V3 v, bool inv) { return inv ? V3{ -v.x, -v.y, v.z } : v; }
+
+DI void put3(float* o, int& k, V3 v)
+{
+    o[k++] = v.x;
+    o[k++] = v.y;
+    o[k++] = v.z;
+}
+
+DI void packCar(const Dev& d, int c, bool inv, float* o, int& k)
+{
+    const Q4 rot = d.cq(CARL_CAR_ROT, c);
+    put3(o, k, mirrorXY(d.cv(CARL_CAR_POS, c), inv));
+    put3(o, k, mirrorXY(d.cv(CARL_CAR_VEL, c), inv));
+    put3(o, k, mirrorXY(d.cv(CARL_CAR_ANG, c), inv));
+    put3(o, k, mirrorXY(rotate(rot, kX), inv));
+    put3(o, k, mirrorXY(rotate(rot, kZ), inv));
+    o[k++] = d.cf(CARL_CAR_BOOST, c);
+    o[k++] = (float)d.ci(CARL_CAR_ON_GROUND, c);
+    o[k++] = (float)(d.ci(CARL_CAR_DEMOED, c) != 0);
+    o[k++] = (float)d.ci(CARL_CAR_HAS_FLIPPED, c);
+    o[k++] = (float)d.ci(CARL_CAR_HAS_DOUBLE_JUMPED, c);
+    o[k++] = (float)d.ci(CARL_CAR_IS_BOOSTING, c);
+}
+
+// one observer's row: ball, self, teammates, opponents, pads, relative
+// vectors, goals, dodge window, controller state [, previous controls]
+DI void packObservation(const Dev& d, int sim, int obs, bool invertOrange, bool normalizeObs, bool prev, float* o)
+{
+    const int nC = d.nCars, base = sim * nC;
+    const bool orange = obs >= d.nBlue;
+    const bool inv = invertOrange && orange;
+    const int ego = base + obs;
+    const V3 ballPos = d.sv(CARL_SIM_BALL_POS, sim), ballVel = d.sv(CARL_SIM_BALL_VEL, sim);
+    const V3 egoPos = d.cv(CARL_CAR_POS, ego), egoVel = d.cv(CARL_CAR_VEL, ego);
+    int k = 0;
+    put3(o, k, mirrorXY(ballPos, inv));
+    put3(o, k, mirrorXY(ballVel, inv));
+    put3(o, k, mirrorXY(d.sv(CARL_SIM_BALL_ANG, sim), inv));
+    packCar(d, ego, inv, o, k);
+    const int tS = orange ? d.nBlue : 0, tE = orange ? nC : d.nBlue;
+    const int oS = orange ? 0 : d.nBlue, oE = orange ? d.nBlue : nC;
+    for (int c = tS; c < tE; c++)
+        if (c != obs) packCar(d, base + c, inv, o, k);
+    for (int c = oS; c < oE; c++) packCar(d, base + c, inv, o, k);
+    for (int p = 0; p < kPads; p++) {
+        const int pi = inv ? mirroredPad(p) : p;
+        o[k++] = d.sf(CARL_SIM_PAD_COOLDOWN + pi, sim) <= 0.f;
+    }
+    for (int p = 0; p < kPads; p++) {
+        const int pi = inv ? mirroredPad(p) : p;
+        o[k++] = len(egoPos - V3{ kPadPos[pi][0], kPadPos[pi][1], kPadPos[pi][2] });
+    }
+    put3(o, k, mirrorXY(ballPos - egoPos, inv));
+    put3(o, k, mirrorXY(ballVel - egoVel, inv));
+    for (int c = tS; c < tE; c++) {
+        if (c == obs) continue;
+        put3(o, k, mirrorXY(d.cv(CARL_CAR_POS, base + c) - egoPos, inv));
+        put3(o, k, mirrorXY(d.cv(CARL_CAR_VEL, base + c) - egoVel, inv));
+    }
+    for (int c = oS; c < oE; c++) {
+        put3(o, k, mirrorXY(d.cv(CARL_CAR_POS, base + c) - egoPos, inv));
+        put3(o, k, mirrorXY(d.cv(CARL_CAR_VEL, base + c) - egoVel, inv));
+    }
+    const float ownY = orange ? kGoalCenterY : -kGoalCenterY;
+    put3(o, k, mirrorXY(V3{ 0.f, ownY, kGoalCenterZ } - ballPos, inv));
+    put3(o, k, mirrorXY(V3{ 0.f, -ownY, kGoalCenterZ } - ballPos, inv));
+    const float atsj = d.cf(CARL_CAR_AIR_TIME_SINCE_JUMP, ego);
+    const bool flip = !d.ci(CARL_CAR_HAS_FLIPPED, ego) && !d.ci(CARL_CAR_HAS_DOUBLE_JUMPED, ego) && atsj < kDoubleJumpWindow;
+    o[k++] = (float)flip;
+    o[k++] = flip ? fmax_(0.f, kDoubleJumpWindow - atsj) : 0.f;
+    o[k++] = (float)d.ci(CARL_CAR_HAS_JUMPED, ego);
+    o[k++] = (float)d.ci(CARL_CAR_IS_JUMPING, ego);
+    o[k++] = (float)d.ci(CARL_CAR_IS_FLIPPING, ego);
+    o[k++] = d.cf(CARL_CAR_FLIP_TIME, ego);
+    o[k++] = d.cf(CARL_CAR_DEMO_TIMER, ego);
+    if (prev) {
+        o[k++] = d.cf(CARL_CAR_CTRL_THROTTLE, ego);
+        o[k++] = d.cf(CARL_CAR_CTRL_STEER, ego);
+        o[k++] = d.cf(CARL_CAR_CTRL_YAW, ego);
+        o[k++] = d.cf(CARL_CAR_CTRL_PITCH, ego);
+        o[k++] = d.cf(CARL_CAR_CTRL_ROLL, ego);
+        o[k++] = (float)d.ci(CARL_CAR_CTRL_JUMP, ego);
+        o[k++] = (float)d.ci(CARL_CAR_CTRL_BOOST, ego);
+        o[k++] = (float)d.ci(CARL_CAR_CTRL_SLIDE, ego);
+    }
+    if (!normalizeObs) return;
+    const V3 scale{ 4108.f, 6000.f, 2076.f };
+    for (int a = 0; a < 3; a++) o[a] /= comp(scale, a);
+    for (int a = 3; a < 6; a++) o[a] /= kBallMaxSpeed;
+    for (int a = 6; a < 9; a++) o[a] /= kBallMaxAng;
+    for (int c = 0; c < nC; c++) {
+        const int off = 9 + c * kObsPerCar;
+        for (int a = 0; a < 3; a++) o[off + a] /= comp(scale, a);
+        for (int a = 3; a < 6; a++) o[off + a] /= kCarMaxSpeed;
+        for (int a = 6; a < 9; a++) o[off + a] /= kCarMaxAng;
+        o[off + 15] /= kBoostMax;
+    }
+    const int dOff = 9 + nC * kObsPerCar + kPads;
+    for (int p = 0; p < kPads; p++) o[dOff + p] /= 14692.54f;
+    int r = dOff + kPads;
+    for (int a = 0; a < 3; a++) {
+        o[r + a] /= 2.f * comp(scale, a);
+        o[r + 3 + a] /= kBallMaxSpeed + kCarMaxSpeed;
+    }
+    r += 6;
+    for (int c = 1; c < nC; c++) {
+        for (int a = 0; a < 3; a++) {
+            o[r + a] /= 2.f * comp(scale, a);
+            o[r + 3 + a] /= 2.f * kCarMaxSpeed;
+        }
+        r += 6;
+    }
+    for (int g = 0; g < 2; g++)
+        for (int a = 0; a < 3; a++) o[r + g * 3 + a] /= 2.f * comp(scale, a);
+}
+
+DI void packStateRow(const Dev& d, int sim, int touchWindow, int tickCount, float* o)
+{
+    int k = 0;
+    put3(o, k, d.sv(CARL_SIM_BALL_POS, sim));
+    put3(o, k, d.sv(CARL_SIM_BALL_VEL, sim));
+    put3(o, k, d.sv(CARL_SIM_BALL_ANG, sim));
+    for (int c = 0; c < d.nCars; c++) {
+        const int car = sim * d.nCars + c;
+        packCar(d, car, false, o, k);
+        o[k++] = d.ci(CARL_CAR_BALL_CONTACT_TICK, car) > tickCount - touchWindow;
+    }
+    for (int p = 0; p < kPads; p++) o[k++] = d.sf(CARL_SIM_PAD_COOLDOWN + p, sim) <= 0.f;
+}
+
+struct DoneRule {
+    int maxTicks, overtimeTicks, noTouchTicks;
+};
+
+DI bool simDone(const Dev& d, int s, int tickCount, DoneRule rule)
+{
+    const int ep = d.si(CARL_SIM_EPISODE_TICKS, s);
+    const int blue = d.si(CARL_SIM_BLUE_SCORE, s), orange = d.si(CARL_SIM_ORANGE_SCORE, s);
+    const bool overtime = d.si(CARL_SIM_OVERTIME, s) != 0;
+    const bool regExpired = ep >= rule.maxTicks && blue != orange;
+    const bool otExpired = overtime && ep >= rule.maxTicks + rule.overtimeTicks;
+    const bool scored = d.si(CARL_SIM_LAST_SCORER, s) != 0;
+    const bool timeout = rule.noTouchTicks > 0 && tickCount - d.si(CARL_SIM_LAST_TOUCH_TICK, s) >= rule.noTouchTicks;
+    return (!overtime && regExpired) || otExpired || timeout || scored;
+}
+
+// ------------------------------------------------------------------ resets
+
+DI void kickoffCar(const Dev& d, int c, int loc, bool invert)
+{
+    const int l = loc % 5;
+    const float x = invert ? -kickoffX(l) : kickoffX(l);
+    const float y = invert ? -kickoffY(l) : kickoffY(l);
+    const float yaw = invert ? kickoffYaw(l) + kPi : kickoffYaw(l);
+    const V3 pos{ x, y, kCarRestZ };
+    const Q4 rot = yawQuat(yaw);
+    d.setv(CARL_CAR_POS, c, pos);
+    d.setv(CARL_CAR_VEL, c, kZero);
+    d.setv(CARL_CAR_ANG, c, kZero);
+    d.setq(CARL_CAR_ROT, c, rot);
+    d.setv(CARL_CAR_CEN, c, pos + rotate(rot, kHitboxOffset));
+    d.setv(CARL_CAR_IMP, c, kZero);
+    d.seti(CARL_CAR_DEMOED, c, 0);
+    d.setf(CARL_CAR_DEMO_TIMER, c, 0.f);
+    d.seti(CARL_CAR_CONTACT_IDX, c, -1);
+    d.setf(CARL_CAR_CONTACT_COOLDOWN, c, 0.f);
+    d.seti(CARL_CAR_BALL_HIT_TICK, c, -1);
+    d.seti(CARL_CAR_BALL_CONTACT_TICK, c, -1);
+    for (int f = CARL_CAR_CTRL_THROTTLE; f <= CARL_CAR_CTRL_SLIDE; f++) d.seti(f, c, 0);
+    for (int k = 0; k < kWheels; k++) d.seti(CARL_CAR_WHEEL_CONTACT + k, c, 0);
+    resetInternal(d, c);
+}
+
+DI void kickoffSim(const Dev& d, int s, int tickCount, int nOrange)
+{
+    const uint32_t seed = mix32((uint32_t)d.seed) ^ mix32((uint32_t)s) ^ mix32((uint32_t)tickCount);
+    const int perm = pickIndex(seed, 120);
+    d.ssetv(CARL_SIM_BALL_POS, s, V3{ 0.f, 0.f, kBallRestZ });
+    d.ssetv(CARL_SIM_BALL_VEL, s, kZero);
+    d.ssetv(CARL_SIM_BALL_ANG, s, kZero);
+    d.sseti(CARL_SIM_BALL_INT_VALID, s, 0);
+    for (int team = 0; team < 2; team++) {
+        const int size = team ? nOrange : d.nBlue;
+        for (int i = 0; i < size; i++) kickoffCar(d, s * d.nCars + team * d.nBlue + i, kickoffSpawn(perm, i), team != 0);
+    }
+}
+
+DI void clearCarContacts(const Dev& d, int c)
+{
+    d.setf(CARL_CAR_BRAKE_STAGE, c, 0.f);
+    d.setf(CARL_CAR_STEER_STAGE, c, 0.f);
+    d.setf(CARL_CAR_DRIVE_STAGE, c, 0.f);
+    d.seti(CARL_CAR_MANIFOLD_COUNT, c, 0);
+    for (int k = 0; k < kWheels; k++) {
+        d.setf(CARL_CAR_LAT_FRICTION + k, c, 0.f);
+        d.setf(CARL_CAR_LON_FRICTION + k, c, 0.f);
+    }
+}
+
+DI void fullResetSim(const Dev& d, int s, int nOrange)
+{
+    d.sseti(CARL_SIM_EPISODE_TICKS, s, 0);
+    d.sseti(CARL_SIM_LAST_TOUCH_TICK, s, 0);
+    d.ssetv(CARL_SIM_BALL_IMP, s, kZero);
+    d.sseti(CARL_SIM_BALL_INT_VALID, s, 0);
+    for (int p = 0; p < kPads; p++) d.ssetf(CARL_SIM_PAD_COOLDOWN + p, s, 0.f);
+    for (int f = CARL_SIM_BLUE_SCORE; f <= CARL_SIM_OVERTIME; f++) d.sseti(f, s, 0);
+    d.sseti(CARL_SIM_BALL_ARENA_CONTACT_TICK, s, -1);
+    for (int k = 0; k < d.nCars; k++) {
+        const int c = s * d.nCars + k;
+        d.setv(CARL_CAR_IMP, c, kZero);
+        d.seti(CARL_CAR_DEMOED, c, 0);
+        d.setf(CARL_CAR_DEMO_TIMER, c, 0.f);
+        d.seti(CARL_CAR_CONTACT_IDX, c, -1);
+        d.setf(CARL_CAR_CONTACT_COOLDOWN, c, 0.f);
+        d.seti(CARL_CAR_BALL_HIT_TICK, c, -1);
+        d.seti(CARL_CAR_BALL_CONTACT_TICK, c, -1);
+        for (int w = 0; w < kWheels; w++) {
+            d.seti(CARL_CAR_WHEEL_SOURCE + w, c, kSrcNone);
+            d.seti(CARL_CAR_WHEEL_CONTACT + w, c, 0);
+        }
+        d.seti(CARL_CAR_ARENA_CONTACT_TICK, c, -1);
+        resetInternal(d, c);
+        clearCarContacts(d, c);
+    }
+    kickoffSim(d, s, 0, nOrange);
+}
+
+DI void resetAfterDone(const Dev& d, int s, int tickCount, DoneRule rule, int nOrange)
+{
+    const bool scored = d.si(CARL_SIM_LAST_SCORER, s) != 0;
+    const int ep = d.si(CARL_SIM_EPISODE_TICKS, s);
+    const bool overtime = d.si(CARL_SIM_OVERTIME, s) != 0;
+    const bool noTouch = rule.noTouchTicks > 0 && tickCount - d.si(CARL_SIM_LAST_TOUCH_TICK, s) >= rule.noTouchTicks;
+    const bool otExpired = overtime && ep >= rule.maxTicks + rule.overtimeTicks;
+    const bool timeout = ep >= rule.maxTicks;
+    if (!overtime && !scored && !noTouch && ep >= rule.maxTicks
+        && d.si(CARL_SIM_BLUE_SCORE, s) == d.si(CARL_SIM_ORANGE_SCORE, s)) {
+        d.sseti(CARL_SIM_OVERTIME, s, 1);
+        return;
+    }
+    if (!(scored || noTouch || otExpired || (!overtime && timeout))) return;
+    for (int f = CARL_SIM_BLUE_SCORE; f <= CARL_SIM_OVERTIME; f++) d.sseti(f, s, 0);
+    kickoffSim(d, s, tickCount, nOrange);
+    d.sseti(CARL_SIM_EPISODE_TICKS, s, 0);
+    d.sseti(CARL_SIM_LAST_TOUCH_TICK, s, tickCount);
+    d.sseti(CARL_SIM_BALL_ARENA_CONTACT_TICK, s, -1);
+    for (int k = 0; k < d.nCars; k++) {
+        const int c = s * d.nCars + k;
+        d.seti(CARL_CAR_ARENA_CONTACT_TICK, c, -1);
+        clearCarContacts(d, c);
+        for (int w = 0; w < kWheels; w++) {
+            d.seti(CARL_CAR_WHEEL_SOURCE + w, c, kSrcNone);
+            d.seti(CARL_CAR_WHEEL_CONTACT + w, c, 0);
+        }
+    }
+    for (int p = 0; p < kPads; p++) d.ssetf(CARL_SIM_PAD_COOLDOWN + p, s, 0.f);
+}
+
+// ----------------------------------------------------------------- setters
+
+struct Selection {
+    const int64_t* indices;
+    const uint8_t* mask;
+    int n;
+};
+
+// target simulation of input row r, or -1 when the row is skipped
+DI int selectRow(const Selection& sel, int r, int nSim)
+{
+    if (sel.mask && !sel.mask[r]) return -1;
+    const int64_t t = sel.indices ? sel.indices[r] : r;
+    return (t < 0 || t >= nSim) ? -1 : (int)t;
+}
+
+DI void setCarRow(const Dev& d, int src, int target, int local, const float* pos, const float* rot, const float* vel,
+                  const float* ang, const void* demoed, bool byteDemoed, const float* boost, const float* internal)
+{
+    const int c = target * d.nCars + local;
+    const float prevBoost = d.cf(CARL_CAR_BOOST, c);
+    const int dm = byteDemoed ? (int)((const uint8_t*)demoed)[src] : ((const int32_t*)demoed)[src];
+    const V3 p{ pos[3 * src], pos[3 * src + 1], pos[3 * src + 2] };
+    const Q4 q{ rot[4 * src], rot[4 * src + 1], rot[4 * src + 2], rot[4 * src + 3] };
+    d.setv(CARL_CAR_POS, c, p);
+    d.setq(CARL_CAR_ROT, c, q);
+    d.setv(CARL_CAR_VEL, c, V3{ vel[3 * src], vel[3 * src + 1], vel[3 * src + 2] });
+    d.setv(CARL_CAR_ANG, c, V3{ ang[3 * src], ang[3 * src + 1], ang[3 * src + 2] });
+    d.setv(CARL_CAR_CEN, c, p + rotate(q, kHitboxOffset));
+    d.setv(CARL_CAR_IMP, c, kZero);
+    d.seti(CARL_CAR_DEMOED, c, dm != 0 ? 1 : 0);
+    d.setf(CARL_CAR_DEMO_TIMER, c, dm ? kDemoRespawnTime + kDt : 0.f);
+    d.seti(CARL_CAR_CONTACT_IDX, c, -1);
+    d.setf(CARL_CAR_CONTACT_COOLDOWN, c, 0.f);
+    d.seti(CARL_CAR_BALL_HIT_TICK, c, -1);
+    d.seti(CARL_CAR_BALL_CONTACT_TICK, c, -1);
+    for (int f = CARL_CAR_CTRL_THROTTLE; f <= CARL_CAR_CTRL_SLIDE; f++) d.seti(f, c, 0);
+    if (internal) {
+        const float* v = internal + (size_t)src * kInternalFields;
+        for (int f = CARL_CAR_ON_GROUND; f <= CARL_CAR_TIME_SINCE_BOOSTED; f++) d.seti(f, c, 0);
+        d.seti(CARL_CAR_ON_GROUND, c, v[0] != 0.f);
+        d.setf(CARL_CAR_AIR_TIME_SINCE_JUMP, c, v[1]);
+        d.setf(CARL_CAR_HANDBRAKE, c, v[2]);
+        d.seti(CARL_CAR_HAS_JUMPED, c, v[3] != 0.f);
+        d.seti(CARL_CAR_IS_JUMPING, c, v[4] != 0.f);
+        d.seti(CARL_CAR_LAST_JUMP, c, v[5] != 0.f);
+        d.setf(CARL_CAR_JUMP_TIME, c, v[6]);
+        d.seti(CARL_CAR_HAS_DOUBLE_JUMPED, c, v[7] != 0.f);
+        d.seti(CARL_CAR_HAS_FLIPPED, c, v[8] != 0.f);
+        d.seti(CARL_CAR_IS_FLIPPING, c, v[9] != 0.f);
+        d.setf(CARL_CAR_FLIP_TIME, c, v[10]);
+        d.seti(CARL_CAR_IS_AUTO_FLIPPING, c, v[11] != 0.f);
+        d.setf(CARL_CAR_AUTO_FLIP_TIMER, c, v[12]);
+        d.setf(CARL_CAR_AUTO_FLIP_SCALE, c, v[13]);
+        d.setv(CARL_CAR_FLIP_TORQUE, c, V3{ v[14], v[15], v[16] });
+        d.seti(CARL_CAR_IS_BOOSTING, c, v[17] != 0.f);
+        d.setf(CARL_CAR_BOOSTING_TIME, c, v[18]);
+        d.setf(CARL_CAR_BOOST, c, boost ? fmin_(kBoostMax, fmax_(0.f, boost[src])) : prevBoost);
+    } else if (boost) {
+        d.setf(CARL_CAR_BOOST, c, fmin_(kBoostMax, fmax_(0.f, boost[src])));
+    }
+    d.seti(CARL_CAR_CTRL_JUMP, c, d.ci(CARL_CAR_LAST_JUMP, c));
+    d.setf(CARL_CAR_BRAKE_STAGE, c, 0.f);
+    d.setf(CARL_CAR_STEER_STAGE, c, 0.f);
+    d.setf(CARL_CAR_DRIVE_STAGE, c, 0.f);
+    d.seti(CARL_CAR_MANIFOLD_COUNT, c, 0);
+    for (int k = 0; k < kWheels; k++) {
+        d.seti(CARL_CAR_WHEEL_CONTACT + k, c, 0);
+        d.setf(CARL_CAR_LAT_FRICTION + k, c, 0.f);
+        d.setf(CARL_CAR_LON_FRICTION + k, c, 0.f);
+    }
+}
+
+// broadphase + suspension raycast against the restored scene; grounded = 3+ wheels
+DI void refreshContacts(const Dev& d, int c)
+{
+    if (d.ci(CARL_CAR_DEMOED, c)) {
+        for (int k = 0; k < kWheels; k++) {
+            d.seti(CARL_CAR_WHEEL_SOURCE + k, c, kSrcNone);
+            d.seti(CARL_CAR_WHEEL_CONTACT + k, c, 0);
+        }
+        d.seti(CARL_CAR_ON_GROUND, c, 0);
+        return;
+    }
+    const V3 cen = d.cv(CARL_CAR_CEN, c);
+    const Q4 rot = d.cq(CARL_CAR_ROT, c);
+    const Broad b = broadphase(d, d.cv(CARL_CAR_POS, c), d.cv(CARL_CAR_VEL, c), d.cv(CARL_CAR_ANG, c), cen, rot);
+    Wheels w;
+    raycast(d, c, c / d.nCars, cen, rot, b, w);
+    storeWheelOutputs(d, c, w);
+    int n = 0;
+    for (int k = 0; k < kWheels; k++) n += (w.src[k] != kSrcNone && w.dist[k] <= wheelRay(k)) ? 1 : 0;
+    d.seti(CARL_CAR_ON_GROUND, c, n >= 3 ? 1 : 0);
+}
+
+}  // namespace carl

@@ -1,0 +1,95 @@
+// state.h - device views of the environment state and the arena.
+//
+// Persistent state lives in two structure-of-arrays blocks of 32-bit words:
+// car plane f, car c at car[f * nTotal + c]; sim plane f, sim s at
+// sim[f * nSim + s] (field numbering of include/carl_amd.h).  A wavefront of
+// 64 consecutive cars therefore reads every field as one contiguous 256-byte
+// segment.  Cars of one simulation are adjacent (c = s * nCars + local).
+//
+// The arena is stored per grid cell: the triangles registered in a cell are a
+// contiguous run of 64-byte records (four float4, one per half cache line
+// pair), so a car walks its cell with unit-stride 16-byte loads and no
+// index -> vertex indirection:
+//   r0 = (v0.x, v0.y, v0.z, e1.x)       e1 = v1 - v0, e2 = v2 - v0
+//   r1 = (e1.y, e1.z, e2.x, e2.y)
+//   r2 = (e2.z, v1.x, v1.y, v1.z)
+//   r3 = (v2.x, v2.y, v2.z, bits(tri | kPlaneFlag))
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "../../include/carl_amd.h"
+#include "constants.h"
+
+namespace carl {
+
+constexpr uint32_t kPlaneFlag = 0x80000000u;  // analytic plane triangle: skipped by the car SAT
+
+struct ArenaView {
+    const float4* rec;       // 4 per cell reference
+    const int* cellStart;    // kCells + 1 offsets into rec (in references)
+    const float4* angles;    // signed edge angles per triangle (xyz)
+};
+
+struct Tri {
+    V3 v0, v1, v2, e1, e2;
+    int idx;
+    bool plane;
+};
+
+DI Tri loadTri(const ArenaView& a, int ref)
+{
+    const float4 r0 = a.rec[4 * ref + 0];
+    const float4 r1 = a.rec[4 * ref + 1];
+    const float4 r2 = a.rec[4 * ref + 2];
+    const float4 r3 = a.rec[4 * ref + 3];
+    Tri t;
+    t.v0 = V3{ r0.x, r0.y, r0.z };
+    t.e1 = V3{ r0.w, r1.x, r1.y };
+    t.e2 = V3{ r1.z, r1.w, r2.x };
+    t.v1 = V3{ r2.y, r2.z, r2.w };
+    t.v2 = V3{ r3.x, r3.y, r3.z };
+    const uint32_t bits = __float_as_uint(r3.w);
+    t.idx = (int)(bits & ~kPlaneFlag);
+    t.plane = (bits & kPlaneFlag) != 0;
+    return t;
+}
+
+HDI void cellOf(V3 p, int& cx, int& cy, int& cz)
+{
+    float x = (p.x - kArenaMin.x) / kCellX;
+    float y = (p.y - kArenaMin.y) / kCellY;
+    float z = (p.z - kArenaMin.z) / kCellZ;
+    x = fmin_(fmax_(x, 0.f), 48.f - 1.f);
+    y = fmin_(fmax_(y, 0.f), 48.f - 1.f);
+    z = fmin_(fmax_(z, 0.f), 10.f - 1.f);
+    cx = (int)x;
+    cy = (int)y;
+    cz = (int)z;
+}
+HDI int flatCell(int cx, int cy, int cz) { return cx + cy * kGridX + cz * kGridX * kGridY; }
+
+struct Dev {
+    uint32_t* car;
+    uint32_t* sim;
+    int nSim, nBlue, nCars, nTotal, seed;
+    ArenaView arena;
+
+    DI float cf(int f, int i) const { return __uint_as_float(car[(size_t)f * nTotal + i]); }
+    DI int ci(int f, int i) const { return (int)car[(size_t)f * nTotal + i]; }
+    DI V3 cv(int f, int i) const { return V3{ cf(f, i), cf(f + 1, i), cf(f + 2, i) }; }
+    DI Q4 cq(int f, int i) const { return Q4{ cf(f, i), cf(f + 1, i), cf(f + 2, i), cf(f + 3, i) }; }
+    DI void setf(int f, int i, float v) const { car[(size_t)f * nTotal + i] = __float_as_uint(v); }
+    DI void seti(int f, int i, int v) const { car[(size_t)f * nTotal + i] = (uint32_t)v; }
+    DI void setv(int f, int i, V3 v) const { setf(f, i, v.x); setf(f + 1, i, v.y); setf(f + 2, i, v.z); }
+    DI void setq(int f, int i, Q4 q) const { setf(f, i, q.x); setf(f + 1, i, q.y); setf(f + 2, i, q.z); setf(f + 3, i, q.w); }
+
+    DI float sf(int f, int s) const { return __uint_as_float(sim[(size_t)f * nSim + s]); }
+    DI int si(int f, int s) const { return (int)sim[(size_t)f * nSim + s]; }
+    DI V3 sv(int f, int s) const { return V3{ sf(f, s), sf(f + 1, s), sf(f + 2, s) }; }
+    DI void ssetf(int f, int s, float v) const { sim[(size_t)f * nSim + s] = __float_as_uint(v); }
+    DI void sseti(int f, int s, int v) const { sim[(size_t)f * nSim + s] = (uint32_t)v; }
+    DI void ssetv(int f, int s, V3 v) const { ssetf(f, s, v.x); ssetf(f + 1, s, v.y); ssetf(f + 2, s, v.z); }
+};
+
+}  // namespace carl

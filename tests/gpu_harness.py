@@ -1,0 +1,124 @@
+"""Engine-vs-oracle harness for the GPU parity tests.
+
+A `Pair` drives the HIP engine (carl_amd._carl.Env) and the CPU oracle with
+identical calls and inputs, and compares every output buffer and the full
+persistent state (include/carl_amd.h layout) field by field.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+import carl_amd
+from abi import CAR_NAMES, SIM_NAMES
+from oracle_py import OracleEnv
+
+OUTPUTS = ("obs", "transition_obs", "state", "transition_state", "rewards", "dones", "score_difference",
+           "episode_ticks", "transition_score_difference", "transition_episode_ticks", "overtime",
+           "transition_overtime")
+
+
+def dev(x: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(x)).to("cuda:0")
+
+
+def gpu_outputs(env) -> dict[str, np.ndarray]:
+    env.synchronize()
+    out = {}
+    for name in OUTPUTS:
+        t = torch.from_dlpack(getattr(env, "get_" + name)())
+        out[name] = t.cpu().numpy().copy()
+    return out
+
+
+def gpu_state(env):
+    car, sim, tick = env.export_state()
+    n_cars = env.n_cars
+    car = np.frombuffer(car, dtype=np.uint32).reshape(len(CAR_NAMES), -1)
+    sim = np.frombuffer(sim, dtype=np.uint32).reshape(len(SIM_NAMES), -1)
+    assert car.shape[1] == env.n_sim * n_cars
+    return car, sim, tick
+
+
+def describe_mismatch(names, a, b, limit=8) -> list[str]:
+    """Per-field report of where two state blocks (planes x items) differ."""
+    lines = []
+    for f in range(a.shape[0]):
+        bad = np.nonzero(a[f] != b[f])[0]
+        if len(bad) == 0:
+            continue
+        fa = a[f].view(np.float32)
+        fb = b[f].view(np.float32)
+        diff = np.abs(fa[bad].astype(np.float64) - fb[bad].astype(np.float64))
+        lines.append(f"{names[f]}: {len(bad)}/{a.shape[1]} differ, first item {bad[0]} "
+                     f"(engine {fa[bad[0]]!r} / {a[f][bad[0]]:#x}, oracle {fb[bad[0]]!r} / {b[f][bad[0]]:#x}), "
+                     f"max |d| {diff.max():.3g}")
+        if len(lines) >= limit:
+            break
+    return lines
+
+
+class Pair:
+    def __init__(self, n_sim, n_blue, n_orange, seed=7, frameskip=1, invert_orange=True, normalize=False,
+                 previous_controls=False):
+        self.gpu = carl_amd.Env(n_sim, n_blue, n_orange, seed, frameskip, invert_orange, normalize,
+                                previous_controls)
+        self.cpu = OracleEnv(n_sim, n_blue, n_orange, seed, frameskip, invert_orange, normalize, previous_controls)
+        self.n_sim, self.n_cars = n_sim, n_blue + n_orange
+
+    def close(self):
+        self.cpu.close()
+        del self.gpu
+
+    # -- mirrored calls
+    def step_continuous(self, actions: np.ndarray):
+        self.gpu.step_continuous(dev(actions))
+        self.cpu.step(np.ascontiguousarray(actions, dtype=np.float32))
+
+    def step_discrete(self, actions: np.ndarray):
+        self.gpu.step(dev(actions.astype(np.int32)))
+        self.cpu.step(np.ascontiguousarray(actions, dtype=np.int32))
+
+    def apply_reset_state(self, values: dict, **kw):
+        gv = {k: dev(v) for k, v in values.items()}
+        gk = {k: (dev(v) if isinstance(v, np.ndarray) else v) for k, v in kw.items()}
+        self.gpu.apply_reset_state(**gv, **gk)
+        self.cpu.apply_reset_state(**values, **kw)
+
+    def set_param(self, name: str, value: int):
+        setattr(self.gpu, name, value)
+        ids = {"max_ticks": 0, "overtime_timeout_ticks": 1, "no_touch_timeout_ticks": 2, "frameskip": 3}
+        self.cpu.set_param(ids[name], value)
+
+    # -- comparisons
+    def output_mismatches(self, names=OUTPUTS, atol=0.0) -> list[str]:
+        g = gpu_outputs(self.gpu)
+        report = []
+        for name in names:
+            a, b = g[name], self.cpu.get(name)
+            a = a.reshape(b.shape)
+            if atol == 0.0:
+                bad = np.nonzero((a != b).reshape(-1))[0] if a.dtype != np.float32 else \
+                    np.nonzero((a.view(np.uint32) != b.view(np.uint32)).reshape(-1))[0]
+            else:
+                bad = np.nonzero((np.abs(a.astype(np.float64) - b.astype(np.float64)) > atol).reshape(-1))[0]
+            if len(bad):
+                i = bad[0]
+                report.append(f"{name}: {len(bad)}/{a.size} differ, first flat index {i} "
+                              f"(engine {a.reshape(-1)[i]!r}, oracle {b.reshape(-1)[i]!r})")
+        return report
+
+    def state_mismatches(self) -> list[str]:
+        gc, gs, gt = gpu_state(self.gpu)
+        oc, os_, ot = self.cpu.export_state()
+        rep = []
+        if gt != ot:
+            rep.append(f"tick counter engine {gt} oracle {ot}")
+        rep += describe_mismatch(CAR_NAMES, gc, oc)
+        rep += describe_mismatch(SIM_NAMES, gs, os_)
+        return rep
+
+    def sync_oracle_from_engine(self):
+        """Copy the engine's persistent state into the oracle."""
+        car, sim, tick = gpu_state(self.gpu)
+        self.cpu.import_state(car, sim, tick)

@@ -1,0 +1,142 @@
+"""HIP engine vs CPU oracle: bit-exact parity on identical inputs.
+
+Both sides follow the same evaluation-order contract (own sin/cos/atan2, no
+FMA contraction, comparison min/max), so every output buffer and every field
+of the persistent state must agree bit for bit after any sequence of calls.
+The workloads restate the benchmark configurations at oracle-sized scale:
+kickoffs, random states (1v1), clustered 3v3, 2v2 with per-step resets, and a
+per-tick resynchronised run that isolates single-tick error.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from carl_amd import workloads
+from gpu_harness import Pair, dev, gpu_state
+
+pytestmark = pytest.mark.gpu
+
+CONTINUOUS = 1
+
+
+def _assert_clean(report, context):
+    if report:
+        pytest.fail(f"{context}:\n  " + "\n  ".join(report))
+
+
+def _lib():
+    from carl_amd import build
+
+    return ctypes.CDLL(str(build.engine_path()))
+
+
+def test_scan_known_answer_and_random(gpu):
+    """Wave64 DPP exclusive scan: {3,1,4,2} -> {0,3,4,8} (tests/direct_controls.cu:15-33)."""
+    lib = _lib()
+    lib.carl_exclusive_scan_i32.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+    rng = np.random.default_rng(3)
+    cases = [np.array([3, 1, 4, 2], np.int32)] + [rng.integers(0, 50, n).astype(np.int32)
+                                                  for n in (1, 63, 64, 65, 2047, 2048, 2049, 100_000, 3_000_000)]
+    for x in cases:
+        src = dev(x)
+        out = torch.full_like(src, -1)
+        assert lib.carl_exclusive_scan_i32(src.data_ptr(), out.data_ptr(), len(x), None) == 0
+        torch.cuda.synchronize()
+        expect = np.concatenate([[0], np.cumsum(x)[:-1]]).astype(np.int32)
+        np.testing.assert_array_equal(out.cpu().numpy(), expect, err_msg=f"n={len(x)}")
+
+
+@pytest.mark.parametrize("teams", [(1, 1), (2, 2), (3, 3), (1, 0), (2, 1)])
+def test_reset_state_and_outputs_match(gpu, teams):
+    p = Pair(33, *teams, seed=11, previous_controls=True)
+    _assert_clean(p.state_mismatches(), f"state after reset {teams}")
+    _assert_clean(p.output_mismatches(), f"outputs after reset {teams}")
+    p.close()
+
+
+def test_kickoff_trajectory_1v1(gpu):
+    rng = np.random.default_rng(1)
+    p = Pair(64, 1, 1, seed=5, frameskip=8)
+    for step in range(40):
+        p.step_continuous(workloads.random_continuous_actions(rng, 64, 2))
+        _assert_clean(p.state_mismatches(), f"state after step {step}")
+        _assert_clean(p.output_mismatches(), f"outputs after step {step}")
+    p.close()
+
+
+def test_random_state_trajectory_1v1(gpu):
+    rng = np.random.default_rng(2)
+    n = 256
+    p = Pair(n, 1, 1, seed=9, frameskip=8, normalize=True)
+    odd = np.arange(1, n, 2)
+    p.apply_reset_state(workloads.random_reset_state(rng, len(odd), 2), simulation_indices=odd.astype(np.int64))
+    _assert_clean(p.state_mismatches(), "state after random reset")
+    for step in range(24):
+        p.step_continuous(workloads.random_continuous_actions(rng, n, 2))
+        _assert_clean(p.state_mismatches(), f"state after step {step}")
+        _assert_clean(p.output_mismatches(), f"outputs after step {step}")
+    p.close()
+
+
+def test_clustered_3v3_contacts(gpu):
+    """Cars within 500 uu of the ball: dense car-car SAT, bumps, demos and ball hits."""
+    rng = np.random.default_rng(4)
+    n = 48
+    p = Pair(n, 3, 3, seed=3, frameskip=8)
+    p.apply_reset_state(workloads.random_reset_state(rng, n, 6, cluster_radius=500.0))
+    _assert_clean(p.state_mismatches(), "state after clustered reset")
+    for step in range(16):
+        p.step_continuous(workloads.random_continuous_actions(rng, n, 6))
+        _assert_clean(p.state_mismatches(), f"state after step {step}")
+        _assert_clean(p.output_mismatches(), f"outputs after step {step}")
+    p.close()
+
+
+def test_2v2_masked_resets_every_step(gpu):
+    """tick_skip 1 with 25% of arenas reset from random states each step (masked path)."""
+    rng = np.random.default_rng(6)
+    n = 64
+    p = Pair(n, 2, 2, seed=13, frameskip=1)
+    for step in range(40):
+        p.step_discrete(workloads.random_discrete_actions(rng, n, 4))
+        mask = rng.uniform(0, 1, n) < 0.25
+        p.apply_reset_state(workloads.random_reset_state(rng, n, 4), reset_mask=mask)
+        _assert_clean(p.state_mismatches(), f"state after step {step}")
+        _assert_clean(p.output_mismatches(), f"outputs after step {step}")
+    p.close()
+
+
+def test_per_tick_from_identical_state(gpu):
+    """Resynchronise the oracle from the engine before every tick; one tick must agree."""
+    rng = np.random.default_rng(8)
+    n = 128
+    p = Pair(n, 2, 2, seed=21, frameskip=1)
+    p.apply_reset_state(workloads.random_reset_state(rng, n, 4, cluster_radius=900.0))
+    for tick in range(60):
+        a = workloads.random_continuous_actions(rng, n, 4)
+        p.sync_oracle_from_engine()
+        p.gpu.tick(dev(a), CONTINUOUS, 1)
+        p.cpu.tick(a, CONTINUOUS, 1)
+        _assert_clean(p.state_mismatches(), f"state after tick {tick}")
+    p.close()
+
+
+def test_long_run_error_growth_1v1(gpu):
+    """1,000 ticks without resynchronisation: report and bound the state error."""
+    rng = np.random.default_rng(10)
+    n = 32
+    p = Pair(n, 1, 1, seed=17, frameskip=8)
+    p.apply_reset_state(workloads.random_reset_state(rng, n, 2))
+    worst = 0.0
+    for step in range(125):
+        p.step_continuous(workloads.random_continuous_actions(rng, n, 2))
+        gc, _, _ = gpu_state(p.gpu)
+        oc, _, _ = p.cpu.export_state()
+        pos_g = gc[0:3].view(np.float32)
+        pos_o = oc[0:3].view(np.float32)
+        worst = max(worst, float(np.abs(pos_g.astype(np.float64) - pos_o).max()))
+    print(f"max car position error over 1000 ticks: {worst:.3g} uu")
+    assert worst <= 1e-3
+    p.close()
