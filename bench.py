@@ -11,8 +11,9 @@ Prints one JSON line:
   value          sim-ticks/s = n_sim * tick_skip * steps / seconds
   roofline       the fused tick kernel: algorithmic bytes (1,488 B per 1v1
                  sim-tick: persistent state read + written + actions) per
-                 launch / average launch time from HIP events on the engine
-                 stream, against 8 TB/s
+                 launch / average launch time, from HIP events the engine
+                 records around every tick launch on its own stream during
+                 the timed steps, against 8 TB/s
   cpu_baseline   the CPU model of the same physics (oracle/liboracle.so), one
                  1v1 arena per thread on this host's cores, direct controls
                  held 8 ticks (bounded sample)
@@ -71,7 +72,6 @@ def main() -> None:
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-ticks", type=int, default=1_200_000,
                     help="CPU-baseline ticks per host thread (0 skips it)")
-    ap.add_argument("--kernel-launches", type=int, default=100)
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -108,28 +108,22 @@ def main() -> None:
     for i in range(args.warmup):
         env_step(i)
     torch.cuda.synchronize()
+    env.enable_tick_timing(True)      # HIP events around every tick-kernel launch
     t0 = time.perf_counter()
     for i in range(args.steps):
         reward = env_step(i)
     torch.cuda.synchronize()
     seconds = time.perf_counter() - t0
+    tick_ms, launches = env.tick_timing()
+    env.enable_tick_timing(False)
     del reward
 
     sim_ticks = n_sim * args.tick_skip * args.steps
     value = sim_ticks / seconds
 
-    # dominant kernel: the fused tick kernel, one launch per frameskip window
-    launches = args.kernel_launches
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    for i in range(3):
-        env.tick(pool[i], 1, args.tick_skip)
-    with torch.cuda.stream(stream):
-        start.record(stream)
-        for i in range(launches):
-            env.tick(pool[i % len(pool)], 1, args.tick_skip)
-        stop.record(stream)
-    stop.synchronize()
-    launch_ms = start.elapsed_time(stop) / launches
+    # dominant kernel: the fused tick kernel, one launch per env step, timed
+    # on the engine stream inside the timed region
+    launch_ms = tick_ms / launches
     launch_bytes = tick_bytes(n_cars) * n_sim * args.tick_skip
     achieved = launch_bytes / (launch_ms * 1e-3) / 1e9
 
@@ -165,6 +159,8 @@ def main() -> None:
             "frac": achieved / HBM_PEAK_GBS,
             "traffic": None,
             "launch_ms": launch_ms,
+            "launches": launches,
+            "tick_kernel_share": tick_ms / (seconds * 1e3),
             "bytes_per_launch": launch_bytes,
         },
     }

@@ -106,17 +106,17 @@ struct TensorView {
     const void* data() const { return static_cast<const char*>(tensor.data) + tensor.byte_offset; }
 };
 
-struct PendingReset {
+struct PendingInput {
     std::vector<py::object> inputs;
     hipEvent_t done = nullptr;
-    explicit PendingReset(std::vector<py::object> in) : inputs(std::move(in))
+    explicit PendingInput(std::vector<py::object> in) : inputs(std::move(in))
     {
         if (hipEventCreateWithFlags(&done, hipEventDisableTiming) != hipSuccess)
             throw std::runtime_error("hipEventCreateWithFlags failed");
     }
-    PendingReset(const PendingReset&) = delete;
-    PendingReset& operator=(const PendingReset&) = delete;
-    ~PendingReset()
+    PendingInput(const PendingInput&) = delete;
+    PendingInput& operator=(const PendingInput&) = delete;
+    ~PendingInput()
     {
         if (done) (void)hipEventDestroy(done);
     }
@@ -125,7 +125,7 @@ struct PendingReset {
 class Env {
     carl_env* env_ = nullptr;
     int nSim_ = 0, nCars_ = 0;
-    std::deque<PendingReset> pending_;
+    std::deque<PendingInput> pending_;
 
     void* stream() const { return carl_env_stream(env_); }
 
@@ -199,7 +199,7 @@ class Env {
         return TensorView{ std::move(cap), t };
     }
 
-    const void* actionData(py::object actions, bool continuous) const
+    TensorView actionData(py::object actions, bool continuous) const
     {
         py::capsule cap = toCapsule(actions, stream());
         const auto* m = cap.get_pointer<DLManagedTensor>();
@@ -215,7 +215,17 @@ class Env {
             throw py::value_error(what + " must have shape [n_sim, n_cars, 7]");
         if (t.strides && (t.strides[2] != 1 || t.strides[1] != kActPerCar || t.strides[0] != nCars_ * kActPerCar))
             throw py::value_error(what + " must be contiguous");
-        return static_cast<const char*>(t.data) + t.byte_offset;
+        return TensorView{ std::move(cap), t };
+    }
+
+    // The engine stream reads caller memory after the call returns; keep the
+    // producer's tensors alive until that stream has passed this point, so a
+    // temporary freed by the caller cannot be reused under a pending read.
+    void holdUntilConsumed(std::vector<py::object> keep)
+    {
+        pending_.emplace_back(std::move(keep));
+        if (hipEventRecord(pending_.back().done, (hipStream_t)stream()) != hipSuccess)
+            throw std::runtime_error("hipEventRecord failed");
     }
 
 public:
@@ -241,16 +251,18 @@ public:
     py::object step(py::object actions)
     {
         releaseInputs();
-        const void* a = actionData(actions, false);
-        check(carl_env_step(env_, CARL_ACTIONS_DISCRETE, a));
+        const TensorView a = actionData(actions, false);
+        check(carl_env_step(env_, CARL_ACTIONS_DISCRETE, a.data()));
+        holdUntilConsumed({ a.capsule });
         return outputCapsule(env_, CARL_BUF_OBS);
     }
 
     py::object stepContinuous(py::object actions)
     {
         releaseInputs();
-        const void* a = actionData(actions, true);
-        check(carl_env_step(env_, CARL_ACTIONS_CONTINUOUS, a));
+        const TensorView a = actionData(actions, true);
+        check(carl_env_step(env_, CARL_ACTIONS_CONTINUOUS, a.data()));
+        holdUntilConsumed({ a.capsule });
         return outputCapsule(env_, CARL_BUF_OBS);
     }
 
@@ -343,8 +355,9 @@ public:
         }
         if (n == 0) return;
         const uint8_t* m = maskView ? (const uint8_t*)maskView->data() : nullptr;
+        std::vector<py::object> keep;
         if (m) {
-            std::vector<py::object> keep = { maskView->capsule, bp.capsule, bv.capsule, ba.capsule, cp.capsule,
+            keep = { maskView->capsule, bp.capsule, bv.capsule, ba.capsule, cp.capsule,
                                              cr.capsule, cv.capsule, ca.capsule, dm.capsule };
             if (bo) keep.push_back(bo->capsule);
             if (in) keep.push_back(in->capsule);
@@ -353,7 +366,6 @@ public:
                 keep.push_back(orr->capsule);
                 keep.push_back(tk->capsule);
             }
-            pending_.emplace_back(std::move(keep));
         }
         check(carl_env_apply_reset(
             env_, (const float*)bp.data(), (const float*)bv.data(), (const float*)ba.data(), (const float*)cp.data(),
@@ -362,8 +374,7 @@ public:
             bl ? (const int32_t*)bl->data() : nullptr, orr ? (const int32_t*)orr->data() : nullptr,
             tk ? (const int32_t*)tk->data() : nullptr, idx, n, m));
         if (m) {
-            if (hipEventRecord(pending_.back().done, (hipStream_t)stream()) != hipSuccess)
-                throw std::runtime_error("hipEventRecord failed");
+            holdUntilConsumed(std::move(keep));
         } else {
             check(carl_env_synchronize(env_));
             pending_.clear();
@@ -444,6 +455,7 @@ public:
 
     void tick(py::object actions, int kind, int n)
     {
+        releaseInputs();
         py::capsule cap = toCapsule(actions, stream());
         const auto* m = cap.get_pointer<DLManagedTensor>();
         if (!m) throw py::value_error("invalid DLPack tensor");
@@ -454,10 +466,19 @@ public:
         const int64_t want = (int64_t)nSim_ * nCars_ * (kind == CARL_ACTIONS_DIRECT ? 8 : 7);
         if (count != want || t.dtype.bits != 32) throw py::value_error("actions have the wrong size");
         check(carl_env_tick(env_, kind, static_cast<const char*>(t.data) + t.byte_offset, n));
+        holdUntilConsumed({ cap });
     }
 
     void resetDones() { check(carl_env_reset_dones(env_)); }
     void synchronize() { check(carl_env_synchronize(env_)); }
+    void enableTiming(bool on) { check(carl_env_enable_timing(env_, on ? 1 : 0)); }
+    py::tuple tickTiming()
+    {
+        double ms = 0.0;
+        int launches = 0;
+        check(carl_env_tick_timing(env_, &ms, &launches));
+        return py::make_tuple(ms, launches);
+    }
 };
 
 }  // namespace
@@ -600,5 +621,7 @@ PYBIND11_MODULE(_carl, m)
         .def("tick", &Env::tick, py::arg("actions"), py::arg("kind"), py::arg("n_ticks") = 1)
         .def("reset_dones", &Env::resetDones)
         .def("synchronize", &Env::synchronize)
+        .def("enable_tick_timing", &Env::enableTiming, py::arg("enable") = true)
+        .def("tick_timing", &Env::tickTiming)
         .def_property_readonly("tick_count", [](Env& e) { return e.param(CARL_PARAM_TICK_COUNT); });
 }

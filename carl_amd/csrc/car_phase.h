@@ -131,46 +131,10 @@ DI bool rayBox(V3 start, V3 dir, V3 center, Q4 rot, float maxDist, float& dist, 
     return true;
 }
 
-// nearest hit per wheel among the cell's triangles, the other cars and the ball
-DI void raycast(const Dev& d, int car, int sim, V3 cen, Q4 rot, Broad b, Wheels& w)
+// rays against the other cars of the simulation, then the ball (after the
+// arena, so only strictly nearer hits replace an arena hit)
+DI void raycastBodies(const Dev& d, int car, int sim, const V3* start, V3 dir, Wheels& w)
 {
-    const V3 up = rotate(rot, kZ);
-    const V3 dir = -up;
-    V3 start[kWheels];
-#pragma unroll
-    for (int k = 0; k < kWheels; k++) {
-        w.dist[k] = wheelRay(k) + 1.f;
-        w.normal[k] = up;
-        w.src[k] = kSrcNone;
-        start[k] = wheelStart(cen, rot, k);
-    }
-    for (int i = 0; i < b.count; i++) {
-        const Tri t = loadTri(d.arena, b.start + i);
-        const V3 pv = cross(dir, t.e2);
-        const float det = dot(t.e1, pv);
-        if (fabsf(det) < 1e-8f) continue;
-        const float invDet = 1.f / det;
-#pragma unroll
-        for (int k = 0; k < kWheels; k++) {
-            const V3 tv = start[k] - t.v0;
-            const float u = invDet * dot(tv, pv);
-            if (u < 0.f || u > 1.f) continue;
-            const V3 qv = cross(tv, t.e1);
-            const float v = invDet * dot(dir, qv);
-            if (v < 0.f || u + v > 1.f) continue;
-            const float hd = invDet * dot(t.e2, qv);
-            if (hd <= 0.f || hd >= w.dist[k]) continue;
-            w.dist[k] = hd;
-            w.src[k] = kSrcArena;
-            V3 fn = cross(t.e1, t.e2);
-            const float nl = lensq(fn);
-            if (nl > 1e-12f) {
-                fn = fn * rsqrt_(nl);
-                if (dot(fn, dir) > 0.f) fn = -fn;
-                w.normal[k] = fn;
-            }
-        }
-    }
     const int base = sim * d.nCars;
     for (int o = 0; o < d.nCars; o++) {
         const int oc = base + o;
@@ -659,26 +623,45 @@ struct Contact {
 };
 
 // Sutherland-Hodgman against one plane; output capped at kMaxPolygon vertices
-// (only reachable through rounding on near-degenerate polygons)
+// (only reachable through rounding on near-degenerate polygons).  The polygon
+// lives in registers: every slot access is unrolled, writes select their slot.
 constexpr int kMaxPolygon = 8;
 
-DI int clipPolygon(const V3* in, int n, V3* out, V3 normal, float dist)
+struct Poly {
+    V3 v[kMaxPolygon];
+    int n;
+};
+
+DI void polyPut(Poly& p, V3 x)
 {
-    if (n == 0) return 0;
-    int o = 0;
-    for (int i = 0; i < n; i++) {
-        const V3 cur = in[i];
-        const V3 nxt = in[i + 1 == n ? 0 : i + 1];
+#pragma unroll
+    for (int j = 0; j < kMaxPolygon; j++)
+        if (j == p.n) p.v[j] = x;
+    p.n++;
+}
+
+DI Poly clipPolygon(const Poly& in, V3 normal, float dist)
+{
+    Poly out;
+#pragma unroll
+    for (int j = 0; j < kMaxPolygon; j++) out.v[j] = kZero;
+    out.n = 0;
+#pragma unroll
+    for (int i = 0; i < kMaxPolygon; i++) {
+        if (i >= in.n) break;
+        const V3 cur = in.v[i];
+        V3 nxt = in.v[0];
+        if (i + 1 < kMaxPolygon && i + 1 < in.n) nxt = in.v[i + 1 < kMaxPolygon ? i + 1 : 0];
         const float cd = dot(normal, cur) - dist;
         const float nd = dot(normal, nxt) - dist;
         const bool ci = cd <= 0.f, ni = nd <= 0.f;
-        if (ci && o < kMaxPolygon) out[o++] = cur;
-        if (ci != ni && o < kMaxPolygon) {
+        if (ci && out.n < kMaxPolygon) polyPut(out, cur);
+        if (ci != ni && out.n < kMaxPolygon) {
             const float t = cd / (cd - nd);
-            out[o++] = cur + (nxt - cur) * t;
+            polyPut(out, cur + (nxt - cur) * t);
         }
     }
-    return o;
+    return out;
 }
 
 DI Contact edgeContact(const LocalTri& t, float minPen, int axisIdx, V3 sep)
@@ -822,8 +805,66 @@ DI void adjustEdgeContact(const LocalTri& t, V3 angles, Contact& ct)
     }
 }
 
-// arena planes plus the deepest triangle contact (Manifold.cuh:198-310)
-DI int buildManifold(const Dev& d, V3 cen, Q4 rot, Broad b, ManPt* pts)
+DI bool nearPoints(const V3* pos, int n, V3 carPos)
+{
+    bool near = false;
+#pragma unroll
+    for (int i = 0; i < kMaxManifold; i++)
+        if (i < n && lensq(pos[i] - carPos) < kManifoldBreakSq) near = true;
+    return near;
+}
+
+// Contacts of one overlapping triangle in generation order (edge contact, or
+// the clipped triangle's vertices against the SAT face); keeps the first with
+// the smallest -depth among those not within break distance of the plane
+// points `near`.  bestVal starts at kFltMax; returns whether one was kept.
+DI bool triBestContact(const LocalTri& t, const Sat& s, const V3* near, int nNear, Contact& best, float& bestVal)
+{
+    bool found = false;
+    if (s.axisIdx >= 4) {
+        const Contact c = edgeContact(t, s.minPen, s.axisIdx, s.minAxis);
+        if (!nearPoints(near, nNear, c.carPos) && -c.depth < bestVal) {
+            bestVal = -c.depth;
+            best = c;
+            found = true;
+        }
+        return found;
+    }
+    Poly poly;
+    poly.v[0] = t.v0; poly.v[1] = t.v1; poly.v[2] = t.v2;
+#pragma unroll
+    for (int j = 3; j < kMaxPolygon; j++) poly.v[j] = kZero;
+    poly.n = 3;
+    const int faceAxis = argmax3(vabs(s.minAxis));
+#pragma unroll
+    for (int a = 0; a < 3; a++) {
+        if (a == faceAxis) continue;
+#pragma unroll
+        for (int sg = 1; sg >= -1; sg -= 2) {
+            if (poly.n > 0) poly = clipPolygon(poly, unitAxis(a) * (float)sg, comp(kHalf, a));
+        }
+    }
+    const V3 faceNormal = unitAxis(faceAxis) * -copysignf(1.f, comp(s.minAxis, faceAxis));
+    const float faceDist = comp(kHalf, faceAxis);
+    const float minDepth = -(s.minPen + kContactBreak);
+#pragma unroll
+    for (int k = 0; k < kMaxPolygon; k++) {
+        if (k >= poly.n) break;
+        float depth = dot(faceNormal, poly.v[k]) - faceDist;
+        depth = fmax_(depth, minDepth);
+        if (depth > kContactBreak) continue;
+        const Contact c{ poly.v[k] + s.minAxis * depth, poly.v[k], s.minAxis, -depth };
+        if (!nearPoints(near, nNear, c.carPos) && -c.depth < bestVal) {
+            bestVal = -c.depth;
+            best = c;
+            found = true;
+        }
+    }
+    return found;
+}
+
+// Analytic arena planes (floor, ceiling, side walls) into the manifold.
+DI int planeManifold(V3 cen, Q4 rot, ManPt* pts)
 {
     int n = 0;
 #pragma unroll
@@ -837,59 +878,177 @@ DI int buildManifold(const Dev& d, V3 cen, Q4 rot, Broad b, ManPt* pts)
         if (dist < kContactBreak && !nearManifold(pts, n, carPos))
             addManifold(pts, n, ManPt{ carPos, worldCar - nrm * dist, nrm, dist });
     }
-
-    Contact best{};
-    float bestDist = kFltMax;
-    int bestRef = -1;
-    int hits = 0;
-    for (int i = 0; i < b.count && hits < kMaxTriHits; i++) {
-        const Tri tri = loadTri(d.arena, b.start + i);
-        if (tri.plane) continue;
-        const LocalTri t = toLocal(tri, cen, rot);
-        const Sat s = boxTriSat(t);
-        if (!s.overlap) continue;
-        hits++;
-        if (s.axisIdx >= 4) {
-            const Contact c = edgeContact(t, s.minPen, s.axisIdx, s.minAxis);
-            if (!nearManifold(pts, n, c.carPos) && -c.depth < bestDist) {
-                bestDist = -c.depth; best = c; bestRef = b.start + i;
-            }
-            continue;
-        }
-        V3 bufA[8], bufB[8];
-        V3* in = bufA;
-        V3* out = bufB;
-        in[0] = t.v0; in[1] = t.v1; in[2] = t.v2;
-        int cnt = 3;
-        const int faceAxis = argmax3(vabs(s.minAxis));
-        for (int a = 0; a < 3 && cnt > 0; a++) {
-            if (a == faceAxis) continue;
-            for (int sg = 1; sg >= -1 && cnt > 0; sg -= 2) {
-                cnt = clipPolygon(in, cnt, out, unitAxis(a) * (float)sg, comp(kHalf, a));
-                V3* sw = in; in = out; out = sw;
-            }
-        }
-        const V3 faceNormal = unitAxis(faceAxis) * -copysignf(1.f, comp(s.minAxis, faceAxis));
-        const float faceDist = comp(kHalf, faceAxis);
-        const float minDepth = -(s.minPen + kContactBreak);
-        for (int k = 0; k < cnt; k++) {
-            float depth = dot(faceNormal, in[k]) - faceDist;
-            depth = fmax_(depth, minDepth);
-            if (depth > kContactBreak) continue;
-            const Contact c{ in[k] + s.minAxis * depth, in[k], s.minAxis, -depth };
-            if (!nearManifold(pts, n, c.carPos) && -c.depth < bestDist) {
-                bestDist = -c.depth; best = c; bestRef = b.start + i;
-            }
-        }
-    }
-    if (bestRef >= 0) {
-        const Tri tri = loadTri(d.arena, bestRef);
-        const LocalTri t = toLocal(tri, cen, rot);
-        const float4 ang = d.arena.angles[tri.idx];
-        adjustEdgeContact(t, V3{ ang.x, ang.y, ang.z }, best);
-        addManifold(pts, n, ManPt{ best.carPos, cen + rotate(rot, best.arenaPos), rotate(rot, best.normal), -best.depth });
-    }
     return n;
+}
+
+// Order key of a contact value (-depth) for the cooperative search: float
+// order, with -0 taken as +0 (the sequential comparison treats them equal),
+// then the candidate position, so the minimum is the first in cell order.
+DI unsigned long long contactKey(float value, int item)
+{
+    if (value == 0.f) value = 0.f;
+    const uint32_t u = __float_as_uint(value);
+    const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)ord << 32) | (uint32_t)item;
+}
+
+// Manifold = arena planes plus the deepest triangle contact (Manifold.cuh:198-310).
+// bestRef is the cell reference holding the deepest contact (found by the
+// cooperative search of the contact kernel), -1 for none; its contact is
+// regenerated here exactly as the search produced it.
+DI int buildManifold(const Dev& d, V3 cen, Q4 rot, int bestRef, ManPt* pts)
+{
+    int n = planeManifold(cen, rot, pts);
+    if (bestRef < 0) return n;
+    V3 near[kMaxManifold];
+#pragma unroll
+    for (int i = 0; i < kMaxManifold; i++) near[i] = pts[i].carPos;
+    const Tri tri = loadTri(d.arena, bestRef);
+    const LocalTri t = toLocal(tri, cen, rot);
+    const Sat s = boxTriSat(t);
+    Contact best{};
+    float bestVal = kFltMax;
+    if (!s.overlap || !triBestContact(t, s, near, n, best, bestVal)) return n;
+    const float4 ang = d.arena.angles[tri.idx];
+    adjustEdgeContact(t, V3{ ang.x, ang.y, ang.z }, best);
+    addManifold(pts, n, ManPt{ best.carPos, cen + rotate(rot, best.arenaPos), rotate(rot, best.normal), -best.depth });
+    return n;
+}
+
+// ------------------------------------------------ cooperative cell search
+//
+// One wave searches the cell runs of its 64 cars together (waveItems): each
+// (car, cell triangle) pair runs the four suspension rays and the car-arena
+// SAT.  Per wheel the nearest ray hit is kept by an LDS atomic minimum of
+// (distance, position in the cell run), which is the sequential result: the
+// reference walks the run in order and keeps strictly nearer hits.  SAT hits
+// are ranked in run order (only the first kMaxTriHits take part, as in the
+// sequential walk) and their contacts compete by contactKey, whose minimum is
+// the first deepest contact of the walk.
+struct ContactLds {
+    int excl[64];
+    int first[64];   // first cell reference of the owner's run
+    int satOn[64];   // owner takes part in the car-arena search (not demoed)
+    float cen[3][64], rot[4][64], dir[3][64];
+    float start[kWheels][3][64];
+    float nearPos[kMaxManifold][3][64];
+    int nearN[64];
+    int satHits[64];
+    unsigned long long rayKey[kWheels][64];
+    unsigned long long bestKey[64];
+};
+
+constexpr unsigned long long kNoKey = ~0ull;
+
+DI void contactItem(const Dev& d, ContactLds& L, int o, int q, int base, int lane)
+{
+    const Tri t = loadTri(d.arena, L.first[o] + q);
+    const V3 dir{ L.dir[0][o], L.dir[1][o], L.dir[2][o] };
+    const V3 pv = cross(dir, t.e2);
+    const float det = dot(t.e1, pv);
+    if (!(fabsf(det) < 1e-8f)) {
+        const float invDet = 1.f / det;
+#pragma unroll
+        for (int k = 0; k < kWheels; k++) {
+            const V3 st{ L.start[k][0][o], L.start[k][1][o], L.start[k][2][o] };
+            const V3 tv = st - t.v0;
+            const float u = invDet * dot(tv, pv);
+            if (u < 0.f || u > 1.f) continue;
+            const V3 qv = cross(tv, t.e1);
+            const float v = invDet * dot(dir, qv);
+            if (v < 0.f || u + v > 1.f) continue;
+            const float hd = invDet * dot(t.e2, qv);
+            if (hd <= 0.f || hd >= wheelRay(k) + 1.f) continue;
+            atomicMin(&L.rayKey[k][o], ((unsigned long long)__float_as_uint(hd) << 32) | (uint32_t)q);
+        }
+    }
+    bool hit = false;
+    LocalTri lt;
+    Sat sat;
+    if (L.satOn[o] && !t.plane) {
+        const V3 cen{ L.cen[0][o], L.cen[1][o], L.cen[2][o] };
+        const Q4 rot{ L.rot[0][o], L.rot[1][o], L.rot[2][o], L.rot[3][o] };
+        lt = toLocal(t, cen, rot);
+        sat = boxTriSat(lt);
+        hit = sat.overlap;
+    }
+    const unsigned long long mask = __ballot(hit);
+    if (!hit) return;
+    // hits of this owner earlier in the run: previous rounds + lower lanes now
+    const int firstLane = L.excl[o] - base > 0 ? L.excl[o] - base : 0;
+    const unsigned long long below = (lane ? (~0ull >> (64 - lane)) : 0ull) & (~0ull << firstLane);
+    const int rank = L.satHits[o] + __popcll(mask & below);
+    if (rank < kMaxTriHits) {
+        V3 near[kMaxManifold];
+#pragma unroll
+        for (int i = 0; i < kMaxManifold; i++) near[i] = V3{ L.nearPos[i][0][o], L.nearPos[i][1][o], L.nearPos[i][2][o] };
+        Contact c;
+        float value = kFltMax;
+        if (triBestContact(lt, sat, near, L.nearN[o], c, value)) atomicMin(&L.bestKey[o], contactKey(value, q));
+    }
+    atomicAdd(&L.satHits[o], 1);
+}
+
+// Owner side, before the search: pose, rays and (with sat) the plane points
+// of the car-arena search into LDS.
+DI void contactPrepare(ContactLds& L, int lane, bool sat, V3 cen, Q4 rot, int first)
+{
+    const V3 dir = -rotate(rot, kZ);
+    L.first[lane] = first;
+    L.satOn[lane] = sat;
+    L.cen[0][lane] = cen.x; L.cen[1][lane] = cen.y; L.cen[2][lane] = cen.z;
+    L.rot[0][lane] = rot.x; L.rot[1][lane] = rot.y; L.rot[2][lane] = rot.z; L.rot[3][lane] = rot.w;
+    L.dir[0][lane] = dir.x; L.dir[1][lane] = dir.y; L.dir[2][lane] = dir.z;
+#pragma unroll
+    for (int k = 0; k < kWheels; k++) {
+        const V3 st = wheelStart(cen, rot, k);
+        L.start[k][0][lane] = st.x; L.start[k][1][lane] = st.y; L.start[k][2][lane] = st.z;
+        L.rayKey[k][lane] = kNoKey;
+    }
+    ManPt pts[kMaxManifold];
+#pragma unroll
+    for (int i = 0; i < kMaxManifold; i++) pts[i] = ManPt{ kZero, kZero, kZero, 0.f };
+    L.nearN[lane] = sat ? planeManifold(cen, rot, pts) : 0;
+#pragma unroll
+    for (int i = 0; i < kMaxManifold; i++) {
+        L.nearPos[i][0][lane] = pts[i].carPos.x; L.nearPos[i][1][lane] = pts[i].carPos.y;
+        L.nearPos[i][2][lane] = pts[i].carPos.z;
+    }
+    L.satHits[lane] = 0;
+    L.bestKey[lane] = kNoKey;
+}
+
+// Owner side, after the search: wheel hits (arena winner, then cars and the
+// ball) and the cell reference of the deepest arena contact (-1 for none).
+DI int contactFinish(const Dev& d, const ContactLds& L, int lane, int car, int sim, V3 cen, Q4 rot, Wheels& w)
+{
+    const V3 up = rotate(rot, kZ);
+    const V3 dir = -up;
+    V3 start[kWheels];
+#pragma unroll
+    for (int k = 0; k < kWheels; k++) {
+        w.dist[k] = wheelRay(k) + 1.f;
+        w.normal[k] = up;
+        w.src[k] = kSrcNone;
+        start[k] = wheelStart(cen, rot, k);
+        const unsigned long long key = L.rayKey[k][lane];
+        if (key == kNoKey) continue;
+        const Tri t = loadTri(d.arena, L.first[lane] + (int)(uint32_t)key);
+        w.dist[k] = __uint_as_float((uint32_t)(key >> 32));
+        w.src[k] = kSrcArena;
+        // arena triangles are non-degenerate (|e1 x e2|^2 > 1e-12 is checked
+        // when the mesh is built), so the winner always sets the normal
+        V3 fn = cross(t.e1, t.e2);
+        const float nl = lensq(fn);
+        if (nl > 1e-12f) {
+            fn = fn * rsqrt_(nl);
+            if (dot(fn, dir) > 0.f) fn = -fn;
+            w.normal[k] = fn;
+        }
+    }
+    raycastBodies(d, car, sim, start, dir, w);
+    const unsigned long long best = L.bestKey[lane];
+    return best == kNoKey ? -1 : L.first[lane] + (int)(uint32_t)best;
 }
 
 // --------------------------------------------------------------- solver body
@@ -1174,14 +1333,14 @@ DI void solveManifold(Body& b, const ManPt* pts, int count)
 }
 
 // suspension, manifold and contact solve of one non-demoed car (Solve.cuh:286-314)
-DI void solveCarArena(const Dev& d, CarRegs& r, const Wheels& w, Broad bp, int tick)
+DI void solveCarArena(const Dev& d, CarRegs& r, const Wheels& w, int bestRef, int tick)
 {
     Body b = makeBody(r.pos, r.vel, r.ang, r.cen, r.rot);
     applySuspension(b, r, w, tick);
     ManPt pts[kMaxManifold];
 #pragma unroll
     for (int i = 0; i < kMaxManifold; i++) pts[i] = ManPt{ kZero, kZero, kZero, 0.f };
-    const int count = buildManifold(d, r.cen, r.rot, bp, pts);
+    const int count = buildManifold(d, r.cen, r.rot, bestRef, pts);
     if (count > 0) {
         solveManifold(b, pts, count);
         if (!(lensq(b.pushVel) == 0.f && lensq(b.turnVel) == 0.f))

@@ -23,6 +23,7 @@
 #include "../../include/carl_amd.h"
 #include "arena.h"
 #include "envio.h"
+#include "wave.h"
 
 using namespace carl;
 
@@ -47,63 +48,151 @@ int fail(int code, const std::string& msg)
 
 constexpr int kTickBlock = 256;
 
-__global__ __launch_bounds__(kTickBlock) void tickKernel(Dev d, int nOrange, int tick0, int nTicks, int kind,
-                                                         const void* __restrict__ actions, int simsPerBlock)
+// Per-tick car workspace between the contact and the car-arena kernels, one
+// plane of nTotal 32-bit words each: wheel hit distance, normal xyz and
+// source per wheel, then the cell reference of the deepest arena contact.
+enum : int { kWsDist = 0, kWsNx = 4, kWsNy = 8, kWsNz = 12, kWsSrc = 16, kWsBest = 20, kWsPlanes = 21 };
+
+// A1: broadphase, suspension raycast and car-arena contact search of every
+// car against the pre-tick poses of the arena, the other cars and the ball.
+// One wave per block; the cell runs of its 64 cars are searched together.
+constexpr int kContactBlock = 64;
+
+__global__ __launch_bounds__(kContactBlock) void contactKernel(Dev d, uint32_t* __restrict__ ws)
+{
+    __shared__ ContactLds L;
+    const int lane = threadIdx.x;
+    const int car = blockIdx.x * kContactBlock + lane;
+    const bool ok = car < d.nTotal;
+    V3 cen = kZero;
+    Q4 rot{ 0.f, 0.f, 0.f, 1.f };
+    Broad bp{ 0, 0 };
+    bool demoed = false;
+    if (ok) {
+        cen = d.cv(CARL_CAR_CEN, car);
+        rot = d.cq(CARL_CAR_ROT, car);
+        bp = broadphase(d, d.cv(CARL_CAR_POS, car), d.cv(CARL_CAR_VEL, car), d.cv(CARL_CAR_ANG, car), cen, rot);
+        demoed = d.ci(CARL_CAR_DEMOED, car) != 0;
+    }
+    contactPrepare(L, lane, ok && !demoed, cen, rot, bp.start);
+    __syncthreads();
+    waveItems(bp.count, L.excl, [&](int o, int q, int base) { contactItem(d, L, o, q, base, lane); });
+    __syncthreads();
+    if (!ok) return;
+    Wheels w;
+    const int best = contactFinish(d, L, lane, car, car / d.nCars, cen, rot, w);
+    const size_t n = d.nTotal;
+#pragma unroll
+    for (int k = 0; k < kWheels; k++) {
+        ws[(kWsDist + k) * n + car] = __float_as_uint(w.dist[k]);
+        ws[(kWsNx + k) * n + car] = __float_as_uint(w.normal[k].x);
+        ws[(kWsNy + k) * n + car] = __float_as_uint(w.normal[k].y);
+        ws[(kWsNz + k) * n + car] = __float_as_uint(w.normal[k].z);
+        ws[(kWsSrc + k) * n + car] = (uint32_t)w.src[k];
+    }
+    ws[kWsBest * n + car] = (uint32_t)best;
+}
+
+// A2: controls, car-arena contacts, suspension and the contact solve.
+__global__ __launch_bounds__(kTickBlock) void carArenaKernel(Dev d, const uint32_t* __restrict__ ws, int kind,
+                                                             const void* __restrict__ actions, int tick)
+{
+    const int car = blockIdx.x * kTickBlock + threadIdx.x;
+    if (car >= d.nTotal) return;
+    const size_t n = d.nTotal;
+    Wheels w;
+#pragma unroll
+    for (int k = 0; k < kWheels; k++) {
+        w.dist[k] = __uint_as_float(ws[(kWsDist + k) * n + car]);
+        w.normal[k] = V3{ __uint_as_float(ws[(kWsNx + k) * n + car]), __uint_as_float(ws[(kWsNy + k) * n + car]),
+                          __uint_as_float(ws[(kWsNz + k) * n + car]) };
+        w.src[k] = (int)ws[(kWsSrc + k) * n + car];
+    }
+    const int best = (int)ws[kWsBest * n + car];
+    const Controls ctl = decodeControls(kind, actions, car);
+    storeWheelOutputs(d, car, w);
+    d.setf(CARL_CAR_CTRL_THROTTLE, car, ctl.throttle);
+    d.setf(CARL_CAR_CTRL_STEER, car, ctl.steer);
+    d.setf(CARL_CAR_CTRL_YAW, car, ctl.yaw);
+    d.setf(CARL_CAR_CTRL_PITCH, car, ctl.pitch);
+    d.setf(CARL_CAR_CTRL_ROLL, car, ctl.roll);
+    d.seti(CARL_CAR_CTRL_JUMP, car, ctl.jump);
+    d.seti(CARL_CAR_CTRL_BOOST, car, ctl.boost);
+    d.seti(CARL_CAR_CTRL_SLIDE, car, ctl.slide);
+    if (d.ci(CARL_CAR_DEMOED, car)) return;
+    CarRegs r;
+    loadRegs(d, car, r);
+    applyControls(r, ctl, w);
+    solveCarArena(d, r, w, best, tick);
+    storeRegs(d, car, r);
+}
+
+// B1: episode clock and the car-car pairs of each simulation, (b, a) with b
+// the later car.
+__global__ __launch_bounds__(kTickBlock) void carCarKernel(Dev d, int tick)
+{
+    const int sim = blockIdx.x * kTickBlock + threadIdx.x;
+    if (sim >= d.nSim) return;
+    d.sseti(CARL_SIM_EPISODE_TICKS, sim, d.si(CARL_SIM_EPISODE_TICKS, sim) + 1);
+    const int base = sim * d.nCars;
+    for (int a = 0; a < d.nCars - 1; a++)
+        for (int b = a + 1; b < d.nCars; b++) carCarPair(d, base + b, base + a, tick);
+}
+
+// B2: ball-arena contacts, car-ball pairs and goal detection.  One wave per
+// block; the arena contacts of its 64 balls are gathered cooperatively.
+constexpr int kBallBlock = 64;
+
+__global__ __launch_bounds__(kBallBlock) void ballKernel(Dev d, int tick)
+{
+    __shared__ BallGatherLds L;
+    const int lane = threadIdx.x;
+    const int sim = blockIdx.x * kBallBlock + lane;
+    const bool ok = sim < d.nSim;
+    const bool awake = ok && !ballSleeping(d, sim);
+    const V3 center = ok ? d.sv(CARL_SIM_BALL_POS, sim) : kZero;
+    int items = 0;
+    bool sequential = false;
+    if (awake) {
+        items = ballGatherRuns(d, center, L, lane);
+        if (items < 0) {
+            sequential = true;
+            items = 0;
+        }
+    }
+    L.cx[lane] = center.x;
+    L.cy[lane] = center.y;
+    L.cz[lane] = center.z;
+    L.hitN[lane] = 0;
+    if (!awake || sequential) L.runs[lane] = 0;
+    __syncthreads();
+    waveItems(items, L.excl, [&](int o, int q, int) { ballGatherItem(d, L, o, q); });
+    __syncthreads();
+    if (!ok) return;
+    BallContact cs[4];
+    int count = 0;
+    if (awake) {
+        if (sequential || L.hitN[lane] > kBallHits) count = gatherBallContacts(d, center, cs);
+        else count = ballContactsFromHits(d, center, L, lane, cs);
+    }
+    ballTick(d, sim, tick, cs, count);
+}
+
+// C + D: integration and impulse caches of every car and ball, then the
+// boost pads of each simulation once all of its cars have moved.  A block
+// owns whole simulations (simsPerBlock * nCars car lanes).
+__global__ __launch_bounds__(kTickBlock) void finishKernel(Dev d, int simsPerBlock)
 {
     const int t = threadIdx.x;
     const int simBase = blockIdx.x * simsPerBlock;
     const int mySim = simBase + t / d.nCars;
-    const bool carOk = t < simsPerBlock * d.nCars && mySim < d.nSim;
     const int car = mySim * d.nCars + t % d.nCars;
     const int laneSim = simBase + t;
+    if (t < simsPerBlock * d.nCars && mySim < d.nSim) finishCar(d, car);
     const bool simOk = t < simsPerBlock && laneSim < d.nSim;
-    Controls ctl{};
-    if (carOk) ctl = decodeControls(kind, actions, car);
-
-    for (int k = 0; k < nTicks; k++) {
-        const int tick = tick0 + k + 1;
-        Wheels w;
-        Broad bp{ 0, 0 };
-        if (carOk) {
-            const V3 cen = d.cv(CARL_CAR_CEN, car);
-            const Q4 rot = d.cq(CARL_CAR_ROT, car);
-            bp = broadphase(d, d.cv(CARL_CAR_POS, car), d.cv(CARL_CAR_VEL, car), d.cv(CARL_CAR_ANG, car), cen, rot);
-            raycast(d, car, mySim, cen, rot, bp, w);
-        }
-        __syncthreads();
-        if (carOk) {
-            storeWheelOutputs(d, car, w);
-            d.setf(CARL_CAR_CTRL_THROTTLE, car, ctl.throttle);
-            d.setf(CARL_CAR_CTRL_STEER, car, ctl.steer);
-            d.setf(CARL_CAR_CTRL_YAW, car, ctl.yaw);
-            d.setf(CARL_CAR_CTRL_PITCH, car, ctl.pitch);
-            d.setf(CARL_CAR_CTRL_ROLL, car, ctl.roll);
-            d.seti(CARL_CAR_CTRL_JUMP, car, ctl.jump);
-            d.seti(CARL_CAR_CTRL_BOOST, car, ctl.boost);
-            d.seti(CARL_CAR_CTRL_SLIDE, car, ctl.slide);
-            if (!d.ci(CARL_CAR_DEMOED, car)) {
-                CarRegs r;
-                loadRegs(d, car, r);
-                applyControls(r, ctl, w);
-                solveCarArena(d, r, w, bp, tick);
-                storeRegs(d, car, r);
-            }
-        }
-        __syncthreads();
-        if (simOk) {
-            d.sseti(CARL_SIM_EPISODE_TICKS, laneSim, d.si(CARL_SIM_EPISODE_TICKS, laneSim) + 1);
-            const int base = laneSim * d.nCars;
-            for (int a = 0; a < d.nCars - 1; a++)
-                for (int b = a + 1; b < d.nCars; b++) carCarPair(d, base + b, base + a, tick);
-            ballTick(d, laneSim, tick);
-        }
-        __syncthreads();
-        if (carOk) finishCar(d, car);
-        if (simOk) finishBall(d, laneSim);
-        __syncthreads();
-        if (simOk) boostPads(d, laneSim);
-        __syncthreads();
-    }
+    if (simOk) finishBall(d, laneSim);
+    __syncthreads();
+    if (simOk) boostPads(d, laneSim);
 }
 
 __global__ void resetKernel(Dev d, int nOrange)
@@ -178,13 +267,39 @@ __global__ void setCarKernel(Dev d, const float* pos, const float* rot, const fl
     setCarRow(d, src, t, src % d.nCars, pos, rot, vel, ang, demoed, byteDemoed != 0, boost, internal);
 }
 
-__global__ void refreshKernel(Dev d, Selection sel)
+// Wheel contacts of the selected cars against the restored scene (rays only,
+// searched cooperatively like the contact kernel).  One wave per block.
+__global__ __launch_bounds__(kContactBlock) void refreshKernel(Dev d, Selection sel)
 {
-    const int src = blockIdx.x * blockDim.x + threadIdx.x;
-    if (src >= sel.n * d.nCars) return;
-    const int t = selectRow(sel, src / d.nCars, d.nSim);
-    if (t < 0) return;
-    refreshContacts(d, t * d.nCars + src % d.nCars);
+    __shared__ ContactLds L;
+    const int lane = threadIdx.x;
+    const int src = blockIdx.x * kContactBlock + lane;
+    int car = -1;
+    if (src < sel.n * d.nCars) {
+        const int t = selectRow(sel, src / d.nCars, d.nSim);
+        if (t >= 0) car = t * d.nCars + src % d.nCars;
+    }
+    const bool active = car >= 0 && !d.ci(CARL_CAR_DEMOED, car);
+    V3 cen = kZero;
+    Q4 rot{ 0.f, 0.f, 0.f, 1.f };
+    Broad bp{ 0, 0 };
+    if (active) {
+        cen = d.cv(CARL_CAR_CEN, car);
+        rot = d.cq(CARL_CAR_ROT, car);
+        bp = broadphase(d, d.cv(CARL_CAR_POS, car), d.cv(CARL_CAR_VEL, car), d.cv(CARL_CAR_ANG, car), cen, rot);
+    }
+    contactPrepare(L, lane, false, cen, rot, bp.start);
+    __syncthreads();
+    waveItems(bp.count, L.excl, [&](int o, int q, int base) { contactItem(d, L, o, q, base, lane); });
+    __syncthreads();
+    if (car < 0) return;
+    if (!active) {
+        clearWheelContacts(d, car);
+        return;
+    }
+    Wheels w;
+    (void)contactFinish(d, L, lane, car, car / d.nCars, cen, rot, w);
+    storeRefreshedWheels(d, car, w);
 }
 
 __global__ void setMatchKernel(Dev d, const int32_t* blue, const int32_t* orange, const int32_t* ticks, Selection sel)
@@ -209,20 +324,8 @@ __global__ void resetPadsKernel(Dev d, Selection sel)
     for (int p = 0; p < kPads; p++) d.ssetf(CARL_SIM_PAD_COOLDOWN + p, t, 0.f);
 }
 
-// ---- wave64 DPP inclusive scan (no library): Hillis-Steele inside each row
-// of 16 lanes with row_shr 1/2/4/8, then row_bcast:15 and row_bcast:31 carry
-// the row totals across the four rows.
-__device__ __forceinline__ int waveInclusiveScan(int v)
-{
-    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
-    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
-    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
-    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
-    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15 -> rows 1,3
-    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31 -> rows 2,3
-    return v;
-}
-
+// ---- exclusive scan (no library): per-tile wave64 DPP scans, tile totals
+// scanned recursively and added back.
 constexpr int kScanBlock = 256;
 constexpr int kScanItems = 8;
 constexpr int kScanTile = kScanBlock * kScanItems;
@@ -317,6 +420,10 @@ struct carl_env {
     int32_t *score = nullptr, *ticks = nullptr, *tscore = nullptr, *tticks = nullptr;
     int32_t* actions = nullptr;
     float* cactions = nullptr;
+    uint32_t* ws = nullptr;  // per-tick car workspace (kWsPlanes planes)
+    bool timing = false;
+    size_t timed = 0;                          // event pairs recorded since the last read
+    std::vector<hipEvent_t> tickStart, tickStop;  // reusable pool
 
     Dev dev() const
     {
@@ -343,9 +450,11 @@ void freeAll(carl_env* e)
 {
     void* ptrs[] = { e->car, e->sim, e->rec, e->cellStart, e->angles, e->obs, e->tobs, e->state, e->tstate,
                      e->rewards, e->dones, e->overtime, e->tovertime, e->score, e->ticks, e->tscore, e->tticks,
-                     e->actions, e->cactions };
+                     e->actions, e->cactions, e->ws };
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
+    for (hipEvent_t ev : e->tickStart) (void)hipEventDestroy(ev);
+    for (hipEvent_t ev : e->tickStop) (void)hipEventDestroy(ev);
     if (e->stream) (void)hipStreamDestroy(e->stream);
 }
 
@@ -354,8 +463,31 @@ int launchTicks(carl_env* e, int kind, const void* actions, int n)
     if (n <= 0) return CARL_OK;
     const int spb = kTickBlock / e->nCars;
     const int blocks = (e->nSim + spb - 1) / spb;
-    tickKernel<<<blocks, spb * e->nCars, 0, e->stream>>>(e->dev(), e->nOrange, e->tickCount, n, kind, actions, spb);
+    if (e->timing) {
+        if (e->timed == e->tickStart.size()) {
+            hipEvent_t a, b;
+            HIP_TRY(hipEventCreate(&a));
+            if (hipEventCreate(&b) != hipSuccess) {
+                (void)hipEventDestroy(a);
+                return fail(CARL_ERR_RUNTIME, "hipEventCreate failed");
+            }
+            e->tickStart.push_back(a);
+            e->tickStop.push_back(b);
+        }
+        HIP_TRY(hipEventRecord(e->tickStart[e->timed], e->stream));
+    }
+    const Dev d = e->dev();
+    const int carBlocks = e->grid(e->nTotal, kTickBlock), simBlocks = e->grid(e->nSim, kTickBlock);
+    for (int k = 0; k < n; k++) {
+        const int tick = e->tickCount + k + 1;
+        contactKernel<<<e->grid(e->nTotal, kContactBlock), kContactBlock, 0, e->stream>>>(d, e->ws);
+        carArenaKernel<<<carBlocks, kTickBlock, 0, e->stream>>>(d, e->ws, kind, actions, tick);
+        carCarKernel<<<simBlocks, kTickBlock, 0, e->stream>>>(d, tick);
+        ballKernel<<<e->grid(e->nSim, kBallBlock), kBallBlock, 0, e->stream>>>(d, tick);
+        finishKernel<<<blocks, spb * e->nCars, 0, e->stream>>>(d, spb);
+    }
     HIP_TRY(hipGetLastError());
+    if (e->timing) HIP_TRY(hipEventRecord(e->tickStop[e->timed++], e->stream));
     e->tickCount += n;
     return CARL_OK;
 }
@@ -433,7 +565,7 @@ int setCarRows(carl_env* e, const float* pos, const float* rot, const float* vel
     setCarKernel<<<e->grid(n, 256), 256, 0, e->stream>>>(e->dev(), pos, rot, vel, ang, demoed, byteDemoed, boost,
                                                           internal, sel);
     HIP_TRY(hipGetLastError());
-    refreshKernel<<<e->grid(n, 256), 256, 0, e->stream>>>(e->dev(), sel);
+    refreshKernel<<<e->grid(n, kContactBlock), kContactBlock, 0, e->stream>>>(e->dev(), sel);
     HIP_TRY(hipGetLastError());
     return CARL_OK;
 }
@@ -528,6 +660,7 @@ int carl_env_create(int nSim, int nBlue, int nOrange, int seed, int frameskip, i
     rc = rc ? rc : devAlloc(&e->tticks, nS);
     rc = rc ? rc : devAlloc(&e->actions, nT * 7);
     rc = rc ? rc : devAlloc(&e->cactions, nT * 7);
+    rc = rc ? rc : devAlloc(&e->ws, nT * kWsPlanes);
     if (rc) return bail(rc);
 
     std::vector<float4> ang(host.angles.size() / 3);
@@ -754,6 +887,32 @@ int carl_env_get_param(carl_env* e, int p, int* v)
     case CARL_PARAM_N_BLUE: *v = e->nBlue; break;
     default: return fail(CARL_ERR_VALUE, "unknown parameter");
     }
+    return CARL_OK;
+}
+
+int carl_env_enable_timing(carl_env* e, int enable)
+{
+    CARL_TRY(checkEnv(e));
+    HIP_TRY(hipStreamSynchronize(e->stream));
+    e->timing = enable != 0;
+    e->timed = 0;
+    return CARL_OK;
+}
+
+int carl_env_tick_timing(carl_env* e, double* totalMs, int* launches)
+{
+    CARL_TRY(checkEnv(e));
+    if (!totalMs || !launches) return fail(CARL_ERR_VALUE, "null output pointer");
+    HIP_TRY(hipStreamSynchronize(e->stream));
+    double sum = 0.0;
+    for (size_t i = 0; i < e->timed; i++) {
+        float ms = 0.f;
+        HIP_TRY(hipEventElapsedTime(&ms, e->tickStart[i], e->tickStop[i]));
+        sum += ms;
+    }
+    *totalMs = sum;
+    *launches = (int)e->timed;
+    e->timed = 0;
     return CARL_OK;
 }
 

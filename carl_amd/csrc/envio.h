@@ -348,22 +348,19 @@ DI void setCarRow(const Dev& d, int src, int target, int local, const float* pos
     }
 }
 
-// broadphase + suspension raycast against the restored scene; grounded = 3+ wheels
-DI void refreshContacts(const Dev& d, int c)
+// after a car restore: a demoed car has no wheel contacts and is airborne
+DI void clearWheelContacts(const Dev& d, int c)
 {
-    if (d.ci(CARL_CAR_DEMOED, c)) {
-        for (int k = 0; k < kWheels; k++) {
-            d.seti(CARL_CAR_WHEEL_SOURCE + k, c, kSrcNone);
-            d.seti(CARL_CAR_WHEEL_CONTACT + k, c, 0);
-        }
-        d.seti(CARL_CAR_ON_GROUND, c, 0);
-        return;
+    for (int k = 0; k < kWheels; k++) {
+        d.seti(CARL_CAR_WHEEL_SOURCE + k, c, kSrcNone);
+        d.seti(CARL_CAR_WHEEL_CONTACT + k, c, 0);
     }
-    const V3 cen = d.cv(CARL_CAR_CEN, c);
-    const Q4 rot = d.cq(CARL_CAR_ROT, c);
-    const Broad b = broadphase(d, d.cv(CARL_CAR_POS, c), d.cv(CARL_CAR_VEL, c), d.cv(CARL_CAR_ANG, c), cen, rot);
-    Wheels w;
-    raycast(d, c, c / d.nCars, cen, rot, b, w);
+    d.seti(CARL_CAR_ON_GROUND, c, 0);
+}
+
+// suspension raycast against the restored scene; grounded = 3+ wheels
+DI void storeRefreshedWheels(const Dev& d, int c, const Wheels& w)
+{
     storeWheelOutputs(d, c, w);
     int n = 0;
     for (int k = 0; k < kWheels; k++) n += (w.src[k] != kSrcNone && w.dist[k] <= wheelRay(k)) ? 1 : 0;

@@ -130,35 +130,39 @@ DI int boxBoxContacts(const Sat& s, const Box& A, const Box& B, PairContact* out
     const V3 eu = boxAxis(inc, au) * comp(kHalf, au);
     const V3 ev = boxAxis(inc, av) * comp(kHalf, av);
     const V3 center = inc.cen + inorm * comp(kHalf, iaxis);
-    V3 bufA[8], bufB[8];
-    bufA[0] = (center - eu) - ev;
-    bufA[1] = (center + eu) - ev;
-    bufA[2] = (center + eu) + ev;
-    bufA[3] = (center - eu) + ev;
-    V3* in = bufA;
-    V3* o = bufB;
-    int cnt = 4;
-    for (int a = 0; a < 3 && cnt > 0; a++) {
-        if (a == faxis) continue;
+    Poly poly;
+    poly.v[0] = (center - eu) - ev;
+    poly.v[1] = (center + eu) - ev;
+    poly.v[2] = (center + eu) + ev;
+    poly.v[3] = (center - eu) + ev;
+#pragma unroll
+    for (int j = 4; j < kMaxPolygon; j++) poly.v[j] = kZero;
+    poly.n = 4;
+#pragma unroll
+    for (int a = 0; a < 3; a++) {
+        if (a == faxis || poly.n == 0) continue;
         const V3 side = boxAxis(ref, a);
         const float ext = comp(kHalf, a);
         const float maxD = dot(ref.cen, side) + ext;
         const float minD = dot(ref.cen, -side) + ext;
-        cnt = clipPolygon(in, cnt, o, side, maxD);
-        { V3* sw = in; in = o; o = sw; }
-        if (cnt == 0) break;
-        cnt = clipPolygon(in, cnt, o, -side, minD);
-        { V3* sw = in; in = o; o = sw; }
+        poly = clipPolygon(poly, side, maxD);
+        if (poly.n == 0) continue;
+        poly = clipPolygon(poly, -side, minD);
     }
     const V3 refCenter = ref.cen + refN * comp(kHalf, faxis);
     int n = 0;
-    for (int i = 0; i < cnt && n < kMaxManifold; i++) {
-        const float depth = dot(refCenter - in[i], refN);
+#pragma unroll
+    for (int i = 0; i < kMaxPolygon; i++) {
+        if (i >= poly.n || n >= kMaxManifold) break;
+        const float depth = dot(refCenter - poly.v[i], refN);
         if (depth < -kContactBreak) continue;
-        const V3 onRef = in[i] + refN * depth;
-        const V3 pA = refIsA ? onRef : in[i];
-        const V3 pB = !refIsA ? onRef : in[i];
-        out[n] = PairContact{ unrotate(A.rot, pA - A.cen), unrotate(B.rot, pB - B.cen), s.minAxis, fmax_(depth, 0.f) };
+        const V3 onRef = poly.v[i] + refN * depth;
+        const V3 pA = refIsA ? onRef : poly.v[i];
+        const V3 pB = !refIsA ? onRef : poly.v[i];
+        const PairContact pc{ unrotate(A.rot, pA - A.cen), unrotate(B.rot, pB - B.cen), s.minAxis, fmax_(depth, 0.f) };
+#pragma unroll
+        for (int j = 0; j < kMaxManifold; j++)
+            if (j == n) out[j] = pc;
         n++;
     }
     if (n > 0) return n;
@@ -595,6 +599,115 @@ DI int gatherBallContacts(const Dev& d, V3 center, BallContact* cs)
     return count;
 }
 
+// ---- cooperative gather: one wave gathers the arena contacts of 64 balls.
+// The cell runs of every ball are flattened over the wave (waveItems); each
+// item is tested with the same conservative box and exact sphere test as the
+// sequential path, and passing triangles are appended to the owner's list.
+// A triangle registered in several of the ball's cells is taken only in the
+// first of them (the low corner of the overlap of its registration box with
+// the ball's cell box), so every list holds distinct triangles.  The owner
+// then sorts its list by triangle index and reduces the contacts in that
+// order, which is exactly what the sequential merge produces: triangles that
+// fail the sphere test add nothing there either.
+constexpr int kBallCells = 12;  // a 186.3 uu box spans at most 3 x 2 x 2 cells
+constexpr int kBallHits = 24;
+
+struct BallGatherLds {
+    int excl[64];
+    int runs[64];
+    int runStart[kBallCells][64];
+    int runFirst[kBallCells][64];
+    int runCell[kBallCells][64];
+    int lo[3][64];
+    float cx[64], cy[64], cz[64];
+    int hitN[64];
+    int hitRef[kBallHits][64];
+    int hitIdx[kBallHits][64];
+};
+
+// Cell runs of one ball into the owner's LDS slots; returns the item count,
+// or -1 when the runs do not fit (the sequential path then gathers).
+DI int ballGatherRuns(const Dev& d, V3 center, BallGatherLds& L, int lane)
+{
+    const float ext = kBallRadius + kBallArenaBreak;
+    int lo[3], hi[3];
+    cellOf(center - ext, lo[0], lo[1], lo[2]);
+    cellOf(center + ext, hi[0], hi[1], hi[2]);
+    int runs = 0, count = 0;
+    for (int z = lo[2]; z <= hi[2]; z++)
+        for (int y = lo[1]; y <= hi[1]; y++)
+            for (int x = lo[0]; x <= hi[0]; x++) {
+                const int cell = flatCell(x, y, z);
+                const int s = d.arena.cellStart[cell], e = d.arena.cellStart[cell + 1];
+                if (e == s) continue;
+                if (runs == kBallCells) return -1;
+                L.runStart[runs][lane] = s;
+                L.runFirst[runs][lane] = count;
+                L.runCell[runs][lane] = cell;
+                runs++;
+                count += e - s;
+            }
+    L.runs[lane] = runs;
+    L.lo[0][lane] = lo[0];
+    L.lo[1][lane] = lo[1];
+    L.lo[2][lane] = lo[2];
+    return count;
+}
+
+DI void ballGatherItem(const Dev& d, BallGatherLds& L, int o, int q)
+{
+    const int nr = L.runs[o];
+    int r = 0;
+    while (r + 1 < nr && L.runFirst[r + 1][o] <= q) r++;
+    const int ref = L.runStart[r][o] + (q - L.runFirst[r][o]);
+    const Tri t = loadTri(d.arena, ref);
+    const V3 center{ L.cx[o], L.cy[o], L.cz[o] };
+    const float reach = kBallRadius + kBallArenaBreak + 1.f;
+    const V3 mn = vmin(vmin(t.v0, t.v1), t.v2);
+    const V3 mx = vmax(vmax(t.v0, t.v1), t.v2);
+    if (center.x < mn.x - reach || center.x > mx.x + reach || center.y < mn.y - reach || center.y > mx.y + reach ||
+        center.z < mn.z - reach || center.z > mx.z + reach)
+        return;
+    // first registration cell of this triangle inside the ball's cell box
+    // (registration spans [cell(min) - 1, cell(max)] per axis, clamped at 0)
+    int rx, ry, rz;
+    cellOf(mn, rx, ry, rz);
+    rx = rx - 1 < 0 ? 0 : rx - 1;
+    ry = ry - 1 < 0 ? 0 : ry - 1;
+    rz = rz - 1 < 0 ? 0 : rz - 1;
+    const int fx = rx > L.lo[0][o] ? rx : L.lo[0][o];
+    const int fy = ry > L.lo[1][o] ? ry : L.lo[1][o];
+    const int fz = rz > L.lo[2][o] ? rz : L.lo[2][o];
+    if (flatCell(fx, fy, fz) != L.runCell[r][o]) return;
+    BallContact ct;
+    if (!sphereTriangle(center, t.v0, t.v1, t.v2, ct)) return;
+    const int slot = atomicAdd(&L.hitN[o], 1);
+    if (slot < kBallHits) {
+        L.hitRef[slot][o] = ref;
+        L.hitIdx[slot][o] = t.idx;
+    }
+}
+
+// Owner side: reduction of the gathered (distinct) hits in triangle order.
+DI int ballContactsFromHits(const Dev& d, V3 center, BallGatherLds& L, int lane, BallContact* cs)
+{
+    const int n = L.hitN[lane];
+    for (int i = 1; i < n; i++) {
+        const int key = L.hitIdx[i][lane], ref = L.hitRef[i][lane];
+        int j = i - 1;
+        while (j >= 0 && L.hitIdx[j][lane] > key) {
+            L.hitIdx[j + 1][lane] = L.hitIdx[j][lane];
+            L.hitRef[j + 1][lane] = L.hitRef[j][lane];
+            j--;
+        }
+        L.hitIdx[j + 1][lane] = key;
+        L.hitRef[j + 1][lane] = ref;
+    }
+    int count = 0;
+    for (int i = 0; i < n; i++) reduceBallContact(d, center, loadTri(d.arena, L.hitRef[i][lane]), cs, count);
+    return count;
+}
+
 struct BallBody {
     V3 vel, velNoExt, ang, dVel, dAng, pushVel, pushAng;
 };
@@ -831,7 +944,14 @@ DI void ballCarPair(const Dev& d, int sim, int c, V3 preBallVel, int tick)
 
 // drag, arena solve, car contacts, integration in Bullet units and goal check
 // (BallArena/Solve.cuh:56-117)
-DI void ballTick(const Dev& d, int sim, int tick)
+DI bool ballSleeping(const Dev& d, int sim)
+{
+    return lensq(d.sv(CARL_SIM_BALL_VEL, sim)) == 0.f && lensq(d.sv(CARL_SIM_BALL_ANG, sim)) == 0.f;
+}
+
+// cs/count: the arena contacts of the exported ball position (unused when
+// the ball sleeps)
+DI void ballTick(const Dev& d, int sim, int tick, const BallContact* cs, int count)
 {
     const V3 ballVel = d.sv(CARL_SIM_BALL_VEL, sim), ballAng = d.sv(CARL_SIM_BALL_ANG, sim);
     const bool sleeping = lensq(ballVel) == 0.f && lensq(ballAng) == 0.f;
@@ -848,8 +968,6 @@ DI void ballTick(const Dev& d, int sim, int tick)
     V3 pushVel = kZero;
     const int base = sim * d.nCars;
     if (!sleeping) {
-        BallContact cs[4];
-        const int count = gatherBallContacts(d, exported, cs);
         bool hit = false;
         for (int k = 0; k < d.nCars; k++) {
             const int h = d.ci(CARL_CAR_BALL_HIT_TICK, base + k);

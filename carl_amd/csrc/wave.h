@@ -1,0 +1,57 @@
+// wave.h - wave64 primitives: DPP prefix sum and a cooperative item loop.
+//
+// The per-car and per-ball candidate lists of one tick vary from a handful
+// of triangles to several hundred, so a lane-per-object loop leaves most of
+// a wavefront idle behind its longest list.  waveItems flattens the lists of
+// all 64 lanes and hands out (owner lane, item) pairs 64 at a time.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace carl {
+
+// Inclusive scan over the 64 lanes: Hillis-Steele inside each row of 16
+// lanes with row_shr 1/2/4/8, then row_bcast:15 and row_bcast:31 carry the
+// row totals across the four rows.
+__device__ __forceinline__ int waveInclusiveScan(int v)
+{
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15 -> rows 1,3
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31 -> rows 2,3
+    return v;
+}
+
+// Calls body(owner, item, base) once for every item < count of every lane of
+// the wave, with all lanes busy.  Items of one owner are visited in ascending
+// order, owners in ascending lane order, 64 consecutive pairs per round; pair
+// j = base + lane runs on `lane` (base is the round's first pair), so the
+// items of one owner in a round sit on consecutive lanes.
+// `excl` is 64 ints of LDS private to this wave.  Every lane of the wave
+// must call it (count 0 for lanes without work).
+template <typename Body>
+__device__ __forceinline__ void waveItems(int count, int* excl, Body&& body)
+{
+    const int lane = (int)(threadIdx.x & 63);
+    const int incl = waveInclusiveScan(count);
+    const int total = __builtin_amdgcn_readlane(incl, 63);
+    excl[lane] = incl - count;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    for (int base = 0; base < total; base += 64) {
+        const int j = base + lane;
+        if (j < total) {
+            // largest owner whose first item is <= j (it has a non-empty list)
+            int o = 0;
+#pragma unroll
+            for (int step = 32; step > 0; step >>= 1)
+                if (excl[o + step] <= j) o += step;
+            body(o, j - excl[o], base);
+        }
+    }
+}
+
+}  // namespace carl

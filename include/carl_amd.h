@@ -30,6 +30,8 @@
  *   carl_env_synchronize   <- cudaStreamSynchronize calls python/carl.cu:419,505,663
  *   carl_exclusive_scan_i32 <- PrefixSum::scanOnStream   src/RLEnvironment.cu:18-38
  *
+ * carl_env_enable_timing / carl_env_tick_timing have no reference counterpart:
+ * they time the tick kernel with HIP events on the environment stream.
  * carl_env_export_state / carl_env_import_state have no reference counterpart;
  * they expose the persistent per-car / per-simulation state (layout below) so
  * that a CPU model can be stepped from the same state and compared field by
@@ -278,6 +280,15 @@ int carl_env_export_state(carl_env* env, uint32_t* car_state, uint32_t* sim_stat
                           int* tick_count);
 int carl_env_import_state(carl_env* env, const uint32_t* car_state,
                           const uint32_t* sim_state, int tick_count);
+
+/* ---- tick-kernel timing (no reference counterpart) -------------------------
+ * With timing enabled, every tick-kernel launch is bracketed by a pair of HIP
+ * events recorded on the environment stream.  carl_env_tick_timing
+ * synchronises that stream, returns the summed launch duration (ms) and the
+ * number of launches since timing was enabled or last read, and clears both.
+ * Enabling or disabling also clears them. */
+int carl_env_enable_timing(carl_env* env, int enable);
+int carl_env_tick_timing(carl_env* env, double* total_ms, int* launches);
 
 /* ---- primitives ------------------------------------------------------------ */
 

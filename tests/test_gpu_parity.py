@@ -66,6 +66,19 @@ def test_kickoff_trajectory_1v1(gpu):
     p.close()
 
 
+def test_queued_steps_with_temporary_actions(gpu):
+    """Steps queued without synchronising, each from a temporary actions tensor
+    the caller drops at once: the engine must read every step's own actions."""
+    rng = np.random.default_rng(12)
+    n = 96
+    p = Pair(n, 1, 1, seed=4, frameskip=8)
+    for _ in range(12):
+        p.step_continuous(workloads.random_continuous_actions(rng, n, 2))
+    _assert_clean(p.state_mismatches(), "state after 12 queued steps")
+    _assert_clean(p.output_mismatches(), "outputs after 12 queued steps")
+    p.close()
+
+
 def test_random_state_trajectory_1v1(gpu):
     rng = np.random.default_rng(2)
     n = 256
