@@ -195,11 +195,12 @@ std::string buildArena(const std::string& objPath, HostArena& out)
         }
     }
 
-    // device records
+    // device records, per triangle and per cell reference
+    if (nTris > kMaxArenaTris) return "arena mesh has more than 65535 triangles";
+    out.triRecords.assign(16 * (size_t)nTris, 0.f);
     const int nRefs = out.cellStart[kCells];
     out.records.assign(16 * (size_t)nRefs, 0.f);
-    for (int r = 0; r < nRefs; r++) {
-        const int t = out.cellTris[r];
+    for (int t = 0; t < nTris; t++) {
         const V3 a = verts[tris[3 * t]], b = verts[tris[3 * t + 1]], c = verts[tris[3 * t + 2]];
         const V3 e1 = b - a, e2 = c - a;
         const bool horizontal = a.z == b.z && a.z == c.z && (a.z == 0.f || a.z == 2048.f);
@@ -209,8 +210,10 @@ std::string buildArena(const std::string& objPath, HostArena& out)
         std::memcpy(&tag, &bits, 4);
         const float rec[16] = { a.x, a.y, a.z, e1.x, e1.y, e1.z, e2.x, e2.y,
                                 e2.z, b.x, b.y, b.z, c.x, c.y, c.z, tag };
-        std::memcpy(&out.records[16 * (size_t)r], rec, sizeof rec);
+        std::memcpy(&out.triRecords[16 * (size_t)t], rec, sizeof rec);
     }
+    for (int r = 0; r < nRefs; r++)
+        std::memcpy(&out.records[16 * (size_t)r], &out.triRecords[16 * (size_t)out.cellTris[r]], 16 * sizeof(float));
     return "";
 }
 

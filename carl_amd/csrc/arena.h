@@ -14,6 +14,7 @@ struct HostArena {
     std::vector<int> cellStart;     // kCells + 1
     std::vector<int> cellTris;      // triangle per cell reference, ascending within a cell
     std::vector<float> records;     // 16 floats per cell reference (device layout, see state.h)
+    std::vector<float> triRecords;  // the same 16 floats per triangle, by triangle index
 };
 
 // Parse, weld and index the mesh.  Returns "" on success, else the error text.

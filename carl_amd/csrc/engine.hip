@@ -415,6 +415,7 @@ struct carl_env {
     float4* rec = nullptr;
     int* cellStart = nullptr;
     float4* angles = nullptr;
+    float4* triRec = nullptr;
     float *obs = nullptr, *tobs = nullptr, *state = nullptr, *tstate = nullptr, *rewards = nullptr;
     bool *dones = nullptr, *overtime = nullptr, *tovertime = nullptr;
     int32_t *score = nullptr, *ticks = nullptr, *tscore = nullptr, *tticks = nullptr;
@@ -429,7 +430,7 @@ struct carl_env {
     {
         Dev d;
         d.car = car; d.sim = sim; d.nSim = nSim; d.nBlue = nBlue; d.nCars = nCars; d.nTotal = nTotal; d.seed = seed;
-        d.arena = ArenaView{ rec, cellStart, angles };
+        d.arena = ArenaView{ rec, cellStart, angles, triRec };
         return d;
     }
     DoneRule rule() const { return DoneRule{ maxTicks, overtimeTicks, noTouchTicks }; }
@@ -448,7 +449,7 @@ int devAlloc(T** p, size_t count)
 
 void freeAll(carl_env* e)
 {
-    void* ptrs[] = { e->car, e->sim, e->rec, e->cellStart, e->angles, e->obs, e->tobs, e->state, e->tstate,
+    void* ptrs[] = { e->car, e->sim, e->rec, e->cellStart, e->angles, e->triRec, e->obs, e->tobs, e->state, e->tstate,
                      e->rewards, e->dones, e->overtime, e->tovertime, e->score, e->ticks, e->tscore, e->tticks,
                      e->actions, e->cactions, e->ws };
     for (void* p : ptrs)
@@ -646,6 +647,7 @@ int carl_env_create(int nSim, int nBlue, int nOrange, int seed, int frameskip, i
     rc = rc ? rc : devAlloc(&e->rec, host.records.size() / 4);
     rc = rc ? rc : devAlloc(&e->cellStart, host.cellStart.size());
     rc = rc ? rc : devAlloc(&e->angles, host.angles.size() / 3);
+    rc = rc ? rc : devAlloc(&e->triRec, host.triRecords.size() / 4);
     rc = rc ? rc : devAlloc(&e->obs, nT * e->obsDim);
     rc = rc ? rc : devAlloc(&e->tobs, nT * e->obsDim);
     rc = rc ? rc : devAlloc(&e->state, nS * e->stateDim);
@@ -669,7 +671,9 @@ int carl_env_create(int nSim, int nBlue, int nOrange, int seed, int frameskip, i
     if (hipMemcpy(e->rec, host.records.data(), host.records.size() * sizeof(float), hipMemcpyHostToDevice) != hipSuccess
         || hipMemcpy(e->cellStart, host.cellStart.data(), host.cellStart.size() * sizeof(int), hipMemcpyHostToDevice)
                != hipSuccess
-        || hipMemcpy(e->angles, ang.data(), ang.size() * sizeof(float4), hipMemcpyHostToDevice) != hipSuccess)
+        || hipMemcpy(e->angles, ang.data(), ang.size() * sizeof(float4), hipMemcpyHostToDevice) != hipSuccess
+        || hipMemcpy(e->triRec, host.triRecords.data(), host.triRecords.size() * sizeof(float), hipMemcpyHostToDevice)
+               != hipSuccess)
         return bail(fail(CARL_ERR_RUNTIME, "arena upload failed"));
 
     rc = fullReset(e);

@@ -610,7 +610,7 @@ DI int gatherBallContacts(const Dev& d, V3 center, BallContact* cs)
 // order, which is exactly what the sequential merge produces: triangles that
 // fail the sphere test add nothing there either.
 constexpr int kBallCells = 12;  // a 186.3 uu box spans at most 3 x 2 x 2 cells
-constexpr int kBallHits = 24;
+constexpr int kBallHits = 64;  // distinct triangles within reach (about 50 at the goal posts)
 
 struct BallGatherLds {
     int excl[64];
@@ -621,8 +621,7 @@ struct BallGatherLds {
     int lo[3][64];
     float cx[64], cy[64], cz[64];
     int hitN[64];
-    int hitRef[kBallHits][64];
-    int hitIdx[kBallHits][64];
+    unsigned short hitIdx[kBallHits][64];  // triangle indices (< kMaxArenaTris)
 };
 
 // Cell runs of one ball into the owner's LDS slots; returns the item count,
@@ -682,10 +681,7 @@ DI void ballGatherItem(const Dev& d, BallGatherLds& L, int o, int q)
     BallContact ct;
     if (!sphereTriangle(center, t.v0, t.v1, t.v2, ct)) return;
     const int slot = atomicAdd(&L.hitN[o], 1);
-    if (slot < kBallHits) {
-        L.hitRef[slot][o] = ref;
-        L.hitIdx[slot][o] = t.idx;
-    }
+    if (slot < kBallHits) L.hitIdx[slot][o] = (unsigned short)t.idx;
 }
 
 // Owner side: reduction of the gathered (distinct) hits in triangle order.
@@ -693,18 +689,16 @@ DI int ballContactsFromHits(const Dev& d, V3 center, BallGatherLds& L, int lane,
 {
     const int n = L.hitN[lane];
     for (int i = 1; i < n; i++) {
-        const int key = L.hitIdx[i][lane], ref = L.hitRef[i][lane];
+        const unsigned short key = L.hitIdx[i][lane];
         int j = i - 1;
         while (j >= 0 && L.hitIdx[j][lane] > key) {
             L.hitIdx[j + 1][lane] = L.hitIdx[j][lane];
-            L.hitRef[j + 1][lane] = L.hitRef[j][lane];
             j--;
         }
         L.hitIdx[j + 1][lane] = key;
-        L.hitRef[j + 1][lane] = ref;
     }
     int count = 0;
-    for (int i = 0; i < n; i++) reduceBallContact(d, center, loadTri(d.arena, L.hitRef[i][lane]), cs, count);
+    for (int i = 0; i < n; i++) reduceBallContact(d, center, loadTriIdx(d.arena, L.hitIdx[i][lane]), cs, count);
     return count;
 }
 

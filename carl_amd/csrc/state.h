@@ -25,10 +25,13 @@ namespace carl {
 
 constexpr uint32_t kPlaneFlag = 0x80000000u;  // analytic plane triangle: skipped by the car SAT
 
+constexpr int kMaxArenaTris = 65535;  // triangle indices are kept in 16 bits in LDS lists
+
 struct ArenaView {
     const float4* rec;       // 4 per cell reference
     const int* cellStart;    // kCells + 1 offsets into rec (in references)
     const float4* angles;    // signed edge angles per triangle (xyz)
+    const float4* tri;       // 4 per triangle, by triangle index (same record layout)
 };
 
 struct Tri {
@@ -37,12 +40,12 @@ struct Tri {
     bool plane;
 };
 
-DI Tri loadTri(const ArenaView& a, int ref)
+DI Tri unpackTri(const float4* rec)
 {
-    const float4 r0 = a.rec[4 * ref + 0];
-    const float4 r1 = a.rec[4 * ref + 1];
-    const float4 r2 = a.rec[4 * ref + 2];
-    const float4 r3 = a.rec[4 * ref + 3];
+    const float4 r0 = rec[0];
+    const float4 r1 = rec[1];
+    const float4 r2 = rec[2];
+    const float4 r3 = rec[3];
     Tri t;
     t.v0 = V3{ r0.x, r0.y, r0.z };
     t.e1 = V3{ r0.w, r1.x, r1.y };
@@ -54,6 +57,9 @@ DI Tri loadTri(const ArenaView& a, int ref)
     t.plane = (bits & kPlaneFlag) != 0;
     return t;
 }
+
+DI Tri loadTri(const ArenaView& a, int ref) { return unpackTri(a.rec + 4 * (size_t)ref); }
+DI Tri loadTriIdx(const ArenaView& a, int idx) { return unpackTri(a.tri + 4 * (size_t)idx); }
 
 HDI void cellOf(V3 p, int& cx, int& cy, int& cz)
 {
