@@ -1,0 +1,63 @@
+"""The C-ABI library without a GPU: it loads, exports every function that
+include/carl_amd.h declares, and its host-only entry points (widths, argument
+validation, error text) behave as documented.  No call here launches work."""
+import ctypes as C
+
+import pytest
+
+from abi import CAR_NAMES, SIM_NAMES, declared_functions, enum_values
+from carl_amd import build
+
+
+@pytest.fixture(scope="module")
+def lib():
+    path = build.engine_path()
+    if not path.is_file():
+        pytest.fail(f"{path} is missing: run __graft_entry__.build()")
+    L = C.CDLL(str(path))
+    L.carl_last_error.restype = C.c_char_p
+    return L
+
+
+def test_every_declared_function_is_exported(lib):
+    names = declared_functions()
+    assert len(names) >= 24
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_widths_match_the_reference_formulas(lib):
+    """include/Cuda/DLPack.h:95-107: obs = 9 + 21n + 68 + 6 + 6(n-1) + 6 + 2 + 5 (+8)."""
+    for n in range(1, 9):
+        base = 9 + 21 * n + 68 + 6 + 6 * (n - 1) + 6 + 2 + 5
+        assert lib.carl_observation_dim(n, 0) == base
+        assert lib.carl_observation_dim(n, 1) == base + 8
+        assert lib.carl_state_dim(n) == 9 + 22 * n + 34
+
+
+def test_state_layout_is_dense():
+    codes = enum_values("CARL_")
+    assert len(CAR_NAMES) == codes["CARL_CAR_FIELDS"] and all(CAR_NAMES)
+    assert len(SIM_NAMES) == codes["CARL_SIM_FIELDS"] and all(SIM_NAMES)
+
+
+@pytest.mark.parametrize("args,message", [
+    ((0, 1, 1, 0, 1, 0), "n_sim must be at least 1"),
+    ((4, 0, 0, 0, 1, 0), "need at least one car"),
+    ((4, 5, 1, 0, 1, 0), "at most 4 cars per team"),
+    ((4, 1, 1, 0, 0, 0), "frameskip must be at least 1"),
+])
+def test_create_rejects_invalid_arguments_before_touching_the_device(lib, args, message):
+    handle = C.c_void_p()
+    rc = lib.carl_env_create(*[C.c_int(a) for a in args], C.byref(handle))
+    assert rc == enum_values("CARL_")["CARL_ERR_VALUE"]
+    assert handle.value is None
+    assert message in lib.carl_last_error().decode()
+
+
+def test_null_handles_are_value_errors(lib):
+    err = enum_values("CARL_")["CARL_ERR_VALUE"]
+    assert lib.carl_env_step(None, 0, None) == err
+    assert lib.carl_env_reset(None) == err
+    assert lib.carl_env_synchronize(None) == err
+    assert "null environment handle" in lib.carl_last_error().decode()
