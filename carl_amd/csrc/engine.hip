@@ -94,7 +94,8 @@ __global__ __launch_bounds__(kContactBlock) void contactKernel(Dev d, uint32_t* 
 }
 
 // A2: controls, car-arena contacts, suspension and the contact solve.
-__global__ __launch_bounds__(kTickBlock) void carArenaKernel(Dev d, const uint32_t* __restrict__ ws, int kind,
+// two waves per SIMD keep all of its waves resident at 65536 1v1 simulations
+__global__ __launch_bounds__(kTickBlock, 2) void carArenaKernel(Dev d, const uint32_t* __restrict__ ws, int kind,
                                                              const void* __restrict__ actions, int tick)
 {
     const int car = blockIdx.x * kTickBlock + threadIdx.x;

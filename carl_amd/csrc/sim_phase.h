@@ -1098,34 +1098,67 @@ DI void finishBall(const Dev& d, int s)
     d.ssetv(CARL_SIM_BALL_IMP, s, kZero);
 }
 
-// pads of one simulation, in pad order; the last overlapping car takes the pad
+// pads of one simulation, in pad order; the last overlapping car takes the pad.
+// The cars' positions, demo flags and boost live in registers for the whole
+// pass (at most kMaxCars per simulation); boosts are written back once.
+constexpr int kMaxCars = 8;
+
 DI void boostPads(const Dev& d, int s)
 {
     const int base = s * d.nCars;
-    for (int p = 0; p < kPads; p++) {
-        float cd = d.sf(CARL_SIM_PAD_COOLDOWN + p, s);
-        if (cd > 0.f) {
-            cd = fmax_(cd - kDt, 0.f);
-            d.ssetf(CARL_SIM_PAD_COOLDOWN + p, s, cd);
+    V3 cp[kMaxCars];
+    bool alive[kMaxCars];
+    float boost[kMaxCars];
+#pragma unroll
+    for (int k = 0; k < kMaxCars; k++) {
+        alive[k] = false;
+        cp[k] = kZero;
+        boost[k] = 0.f;
+        if (k < d.nCars) {
+            alive[k] = !d.ci(CARL_CAR_DEMOED, base + k);
+            cp[k] = d.cv(CARL_CAR_POS, base + k);
+            boost[k] = d.cf(CARL_CAR_BOOST, base + k);
         }
-        if (cd > 0.f) continue;
-        const bool big = p < 6;
-        const float radius = big ? kBigPadRadius : kSmallPadRadius;
-        const float px = kPadPos[p][0], py = kPadPos[p][1], pz = kPadPos[p][2];
-        int locked = -1;
-        for (int k = 0; k < d.nCars; k++) {
-            const int c = base + k;
-            if (d.ci(CARL_CAR_DEMOED, c)) continue;
-            const V3 cp = d.cv(CARL_CAR_POS, c);
-            const float dx = cp.x - px, dy = cp.y - py;
-            if (dx * dx + dy * dy < radius * radius && fabsf(cp.z - pz) < kPadHeight) locked = c;
-        }
-        if (locked < 0) continue;
-        const float boost = d.cf(CARL_CAR_BOOST, locked);
-        if (boost >= kBoostMax) continue;
-        d.setf(CARL_CAR_BOOST, locked, fmin_(boost + (big ? kBigPadAmount : kSmallPadAmount), kBoostMax));
-        d.ssetf(CARL_SIM_PAD_COOLDOWN + p, s, big ? kBigPadCooldown : kSmallPadCooldown);
     }
+    // all cooldowns are read before any is written back
+    float cool[kPads];
+#pragma unroll
+    for (int p = 0; p < kPads; p++) cool[p] = d.sf(CARL_SIM_PAD_COOLDOWN + p, s);
+    int changed = 0;
+#pragma unroll
+    for (int p = 0; p < kPads; p++) {
+        const float prev = cool[p];
+        float cd = prev;
+        if (cd > 0.f) cd = fmax_(cd - kDt, 0.f);
+        if (cd <= 0.f) {
+            const bool big = p < 6;
+            const float radius = big ? kBigPadRadius : kSmallPadRadius;
+            const float px = kPadPos[p][0], py = kPadPos[p][1], pz = kPadPos[p][2];
+            int locked = -1;
+            float have = 0.f;
+#pragma unroll
+            for (int k = 0; k < kMaxCars; k++) {
+                if (k >= d.nCars || !alive[k]) continue;
+                const float dx = cp[k].x - px, dy = cp[k].y - py;
+                if (dx * dx + dy * dy < radius * radius && fabsf(cp[k].z - pz) < kPadHeight) {
+                    locked = k;
+                    have = boost[k];
+                }
+            }
+            if (locked >= 0 && have < kBoostMax) {
+                const float next = fmin_(have + (big ? kBigPadAmount : kSmallPadAmount), kBoostMax);
+#pragma unroll
+                for (int k = 0; k < kMaxCars; k++)
+                    if (k == locked) boost[k] = next;
+                changed |= 1 << locked;
+                cd = big ? kBigPadCooldown : kSmallPadCooldown;
+            }
+        }
+        if (__float_as_uint(cd) != __float_as_uint(prev)) d.ssetf(CARL_SIM_PAD_COOLDOWN + p, s, cd);
+    }
+#pragma unroll
+    for (int k = 0; k < kMaxCars; k++)
+        if (changed & (1 << k)) d.setf(CARL_CAR_BOOST, base + k, boost[k]);
 }
 
 }  // namespace carl
