@@ -472,12 +472,15 @@ public:
     void resetDones() { check(carl_env_reset_dones(env_)); }
     void synchronize() { check(carl_env_synchronize(env_)); }
     void enableTiming(bool on) { check(carl_env_enable_timing(env_, on ? 1 : 0)); }
-    py::tuple tickTiming()
+    py::dict tickTiming()
     {
-        double ms = 0.0;
-        int launches = 0;
-        check(carl_env_tick_timing(env_, &ms, &launches));
-        return py::make_tuple(ms, launches);
+        double ms[CARL_TICK_KERNELS];
+        int launches[CARL_TICK_KERNELS];
+        check(carl_env_tick_timing(env_, ms, launches));
+        py::dict out;
+        for (int k = 0; k < CARL_TICK_KERNELS; k++)
+            out[py::str(carl_tick_kernel_name(k))] = py::make_tuple(ms[k], launches[k]);
+        return out;
     }
 };
 

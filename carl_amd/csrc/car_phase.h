@@ -575,8 +575,8 @@ DI LocalTri toLocal(const Tri& t, V3 cen, Q4 rot)
     return l;
 }
 
-DI V3 triVert(const LocalTri& t, int i) { return i == 0 ? t.v0 : (i == 1 ? t.v1 : t.v2); }
-DI V3 triEdge(const LocalTri& t, int i) { return i == 0 ? t.e0 : (i == 1 ? t.e1 : t.e2); }
+DI V3 triVert(const LocalTri& t, int i) { return sel(i == 0, t.v0, sel(i == 1, t.v1, t.v2)); }
+DI V3 triEdge(const LocalTri& t, int i) { return sel(i == 0, t.e0, sel(i == 1, t.e1, t.e2)); }
 
 struct Sat {
     bool overlap;
@@ -634,9 +634,7 @@ struct Poly {
 
 DI void polyPut(Poly& p, V3 x)
 {
-#pragma unroll
-    for (int j = 0; j < kMaxPolygon; j++)
-        if (j == p.n) p.v[j] = x;
+    setAt(p.v, p.n, x);
     p.n++;
 }
 
@@ -706,6 +704,12 @@ struct ManPt {
     float dist;
 };
 
+DI ManPt sel(bool c, const ManPt& a, const ManPt& b)
+{
+    return ManPt{ sel(c, a.carPos, b.carPos), sel(c, a.worldPos, b.worldPos), sel(c, a.worldNormal, b.worldNormal),
+                  sel(c, a.dist, b.dist) };
+}
+
 constexpr float kManifoldBreakSq = kContactBreak * kContactBreak;
 
 DI bool nearManifold(const ManPt* pts, int n, V3 carPos)
@@ -743,8 +747,7 @@ DI void addManifold(ManPt* pts, int& n, const ManPt& p)
     const int idx = n == kMaxManifold ? replacementSlot(pts, p) : n;
     if (n < kMaxManifold) n++;
 #pragma unroll
-    for (int i = 0; i < kMaxManifold; i++)
-        if (i == idx) pts[i] = p;
+    for (int i = 0; i < kMaxManifold; i++) pts[i] = sel(i == idx, p, pts[i]);
 }
 
 DI bool clampEdgeNormal(V3 edgeAxis, V3 faceN, V3 contactN, float edgeAngle, V3& out)

@@ -94,9 +94,25 @@ HDI V3 normalize(V3 a) { return a / len(a); }
 HDI V3 vmin(V3 a, V3 b) { return V3{ fmin_(a.x, b.x), fmin_(a.y, b.y), fmin_(a.z, b.z) }; }
 HDI V3 vmax(V3 a, V3 b) { return V3{ fmax_(a.x, b.x), fmax_(a.y, b.y), fmax_(a.z, b.z) }; }
 HDI float comp(V3 a, int i) { return i == 0 ? a.x : (i == 1 ? a.y : a.z); }
+// Member-wise select: a plain ?: on an aggregate selects between the two
+// addresses and copies through memory, which pins both into scratch.
+HDI float sel(bool c, float a, float b) { return c ? a : b; }
+HDI V3 sel(bool c, V3 a, V3 b) { return V3{ c ? a.x : b.x, c ? a.y : b.y, c ? a.z : b.z }; }
+
+// a[idx] = v for a small register array: every slot is rewritten through a
+// member-wise select, so no dynamic address is formed and the array stays in
+// registers (a conditional store per slot can be merged into one indexed
+// store, which forces the array into scratch memory).
+template <typename T, int N>
+HDI void setAt(T (&a)[N], int idx, const T& v)
+{
+#pragma unroll
+    for (int j = 0; j < N; j++) a[j] = sel(j == idx, v, a[j]);
+}
+
 HDI void setComp(V3& a, int i, float v) { if (i == 0) a.x = v; else if (i == 1) a.y = v; else a.z = v; }
 HDI int argmax3(V3 a) { return a.y > a.x ? (a.y > a.z ? 1 : 2) : (a.x > a.z ? 0 : 2); }
-HDI V3 unitAxis(int i) { return i == 0 ? V3{ 1.f, 0.f, 0.f } : (i == 1 ? V3{ 0.f, 1.f, 0.f } : V3{ 0.f, 0.f, 1.f }); }
+HDI V3 unitAxis(int i) { return V3{ i == 0 ? 1.f : 0.f, i == 1 ? 1.f : 0.f, i == 2 || (i != 0 && i != 1) ? 1.f : 0.f }; }
 constexpr V3 kZero{ 0.f, 0.f, 0.f };
 constexpr V3 kX{ 1.f, 0.f, 0.f };
 constexpr V3 kY{ 0.f, 1.f, 0.f };

@@ -424,8 +424,10 @@ struct carl_env {
     float* cactions = nullptr;
     uint32_t* ws = nullptr;  // per-tick car workspace (kWsPlanes planes)
     bool timing = false;
-    size_t timed = 0;                          // event pairs recorded since the last read
-    std::vector<hipEvent_t> tickStart, tickStop;  // reusable pool
+    // timing markers: per timed tick, one event before each tick kernel and
+    // one after the last (CARL_TICK_KERNELS + 1); reusable pool
+    size_t timedTicks = 0;
+    std::vector<hipEvent_t> marks;
 
     Dev dev() const
     {
@@ -455,41 +457,55 @@ void freeAll(carl_env* e)
                      e->actions, e->cactions, e->ws };
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
-    for (hipEvent_t ev : e->tickStart) (void)hipEventDestroy(ev);
-    for (hipEvent_t ev : e->tickStop) (void)hipEventDestroy(ev);
+    for (hipEvent_t ev : e->marks) (void)hipEventDestroy(ev);
     if (e->stream) (void)hipStreamDestroy(e->stream);
 }
+
+constexpr int kMarksPerTick = CARL_TICK_KERNELS + 1;
+
+// Timing marker i of the current tick (events are created on first use).
+int mark(carl_env* e, int i)
+{
+    if (!e->timing) return CARL_OK;
+    const size_t slot = e->timedTicks * kMarksPerTick + i;
+    while (e->marks.size() <= slot) {
+        hipEvent_t ev;
+        HIP_TRY(hipEventCreate(&ev));
+        e->marks.push_back(ev);
+    }
+    HIP_TRY(hipEventRecord(e->marks[slot], e->stream));
+    return CARL_OK;
+}
+
+#define CARL_MARK(i)                      \
+    do {                                  \
+        const int rc_ = mark(e, (i));     \
+        if (rc_ != CARL_OK) return rc_;   \
+    } while (0)
 
 int launchTicks(carl_env* e, int kind, const void* actions, int n)
 {
     if (n <= 0) return CARL_OK;
     const int spb = kTickBlock / e->nCars;
     const int blocks = (e->nSim + spb - 1) / spb;
-    if (e->timing) {
-        if (e->timed == e->tickStart.size()) {
-            hipEvent_t a, b;
-            HIP_TRY(hipEventCreate(&a));
-            if (hipEventCreate(&b) != hipSuccess) {
-                (void)hipEventDestroy(a);
-                return fail(CARL_ERR_RUNTIME, "hipEventCreate failed");
-            }
-            e->tickStart.push_back(a);
-            e->tickStop.push_back(b);
-        }
-        HIP_TRY(hipEventRecord(e->tickStart[e->timed], e->stream));
-    }
     const Dev d = e->dev();
     const int carBlocks = e->grid(e->nTotal, kTickBlock), simBlocks = e->grid(e->nSim, kTickBlock);
     for (int k = 0; k < n; k++) {
         const int tick = e->tickCount + k + 1;
+        CARL_MARK(CARL_KERNEL_CONTACT);
         contactKernel<<<e->grid(e->nTotal, kContactBlock), kContactBlock, 0, e->stream>>>(d, e->ws);
+        CARL_MARK(CARL_KERNEL_CAR_ARENA);
         carArenaKernel<<<carBlocks, kTickBlock, 0, e->stream>>>(d, e->ws, kind, actions, tick);
+        CARL_MARK(CARL_KERNEL_CAR_CAR);
         carCarKernel<<<simBlocks, kTickBlock, 0, e->stream>>>(d, tick);
+        CARL_MARK(CARL_KERNEL_BALL);
         ballKernel<<<e->grid(e->nSim, kBallBlock), kBallBlock, 0, e->stream>>>(d, tick);
+        CARL_MARK(CARL_KERNEL_FINISH);
         finishKernel<<<blocks, spb * e->nCars, 0, e->stream>>>(d, spb);
+        CARL_MARK(CARL_TICK_KERNELS);
+        if (e->timing) e->timedTicks++;
     }
     HIP_TRY(hipGetLastError());
-    if (e->timing) HIP_TRY(hipEventRecord(e->tickStop[e->timed++], e->stream));
     e->tickCount += n;
     return CARL_OK;
 }
@@ -900,25 +916,35 @@ int carl_env_enable_timing(carl_env* e, int enable)
     CARL_TRY(checkEnv(e));
     HIP_TRY(hipStreamSynchronize(e->stream));
     e->timing = enable != 0;
-    e->timed = 0;
+    e->timedTicks = 0;
     return CARL_OK;
 }
 
-int carl_env_tick_timing(carl_env* e, double* totalMs, int* launches)
+int carl_env_tick_timing(carl_env* e, double* kernelMs, int* launches)
 {
     CARL_TRY(checkEnv(e));
-    if (!totalMs || !launches) return fail(CARL_ERR_VALUE, "null output pointer");
+    if (!kernelMs || !launches) return fail(CARL_ERR_VALUE, "null output pointer");
     HIP_TRY(hipStreamSynchronize(e->stream));
-    double sum = 0.0;
-    for (size_t i = 0; i < e->timed; i++) {
-        float ms = 0.f;
-        HIP_TRY(hipEventElapsedTime(&ms, e->tickStart[i], e->tickStop[i]));
-        sum += ms;
+    for (int k = 0; k < CARL_TICK_KERNELS; k++) {
+        kernelMs[k] = 0.0;
+        launches[k] = (int)e->timedTicks;
     }
-    *totalMs = sum;
-    *launches = (int)e->timed;
-    e->timed = 0;
+    for (size_t t = 0; t < e->timedTicks; t++) {
+        for (int k = 0; k < CARL_TICK_KERNELS; k++) {
+            float ms = 0.f;
+            HIP_TRY(hipEventElapsedTime(&ms, e->marks[t * kMarksPerTick + k], e->marks[t * kMarksPerTick + k + 1]));
+            kernelMs[k] += ms;
+        }
+    }
+    e->timedTicks = 0;
     return CARL_OK;
+}
+
+const char* carl_tick_kernel_name(int kernel)
+{
+    static const char* names[CARL_TICK_KERNELS] = { "contactKernel", "carArenaKernel", "carCarKernel", "ballKernel",
+                                                    "finishKernel" };
+    return kernel >= 0 && kernel < CARL_TICK_KERNELS ? names[kernel] : "";
 }
 
 int carl_env_export_state(carl_env* e, uint32_t* car, uint32_t* sim, int* tick)

@@ -23,6 +23,12 @@ struct Box {
     Q4 rot;
 };
 
+DI Box sel(bool c, const Box& a, const Box& b)
+{
+    return Box{ sel(c, a.cen, b.cen),
+                Q4{ c ? a.rot.x : b.rot.x, c ? a.rot.y : b.rot.y, c ? a.rot.z : b.rot.z, c ? a.rot.w : b.rot.w } };
+}
+
 DI V3 boxAxis(const Box& b, int i) { return rotate(b.rot, unitAxis(i)); }
 
 DI V3 boxSupport(const Box& b, V3 dir)
@@ -96,6 +102,12 @@ struct PairContact {
     float depth;
 };
 
+DI PairContact sel(bool c, const PairContact& a, const PairContact& b)
+{
+    return PairContact{ sel(c, a.posA, b.posA), sel(c, a.posB, b.posB), sel(c, a.normal, b.normal),
+                        sel(c, a.depth, b.depth) };
+}
+
 // reference face clipping or support-point contact (CarCar/Clip.cuh:25-197)
 DI int boxBoxContacts(const Sat& s, const Box& A, const Box& B, PairContact* out)
 {
@@ -106,8 +118,8 @@ DI int boxBoxContacts(const Sat& s, const Box& A, const Box& B, PairContact* out
         return 1;
     }
     const bool refIsA = s.axisIdx < 3;
-    const Box& ref = refIsA ? A : B;
-    const Box& inc = refIsA ? B : A;
+    const Box ref = sel(refIsA, A, B);
+    const Box inc = sel(refIsA, B, A);
     const int faxis = refIsA ? s.axisIdx : s.axisIdx - 3;
     V3 refN = boxAxis(ref, faxis);
     if (dot(refN, inc.cen - ref.cen) < 0.f) refN = -refN;
@@ -161,8 +173,7 @@ DI int boxBoxContacts(const Sat& s, const Box& A, const Box& B, PairContact* out
         const V3 pB = !refIsA ? onRef : poly.v[i];
         const PairContact pc{ unrotate(A.rot, pA - A.cen), unrotate(B.rot, pB - B.cen), s.minAxis, fmax_(depth, 0.f) };
 #pragma unroll
-        for (int j = 0; j < kMaxManifold; j++)
-            if (j == n) out[j] = pc;
+        for (int j = 0; j < kMaxManifold; j++) out[j] = sel(j == n, pc, out[j]);
         n++;
     }
     if (n > 0) return n;
@@ -275,11 +286,13 @@ DI float bumpCurve(float s, float lo, float mid, float hi)
 DI bool frontHit(const PairContact* cts, int count, bool aIsBumper, V3 delta, Q4 bumperRot)
 {
     if (unrotate(bumperRot, delta).x > kBumpMinForward) return true;
-    for (int i = 0; i < count; i++) {
-        const V3 p = aIsBumper ? cts[i].posA : cts[i].posB;
-        if (p.x + kHitboxOffset.x > kBumpMinForward) return true;
+    bool hit = false;
+#pragma unroll
+    for (int i = 0; i < kMaxManifold; i++) {
+        const float px = aIsBumper ? cts[i].posA.x : cts[i].posB.x;
+        if (i < count && px + kHitboxOffset.x > kBumpMinForward) hit = true;
     }
-    return false;
+    return hit;
 }
 
 DI Body loadBody(const Dev& d, int c)
@@ -399,6 +412,12 @@ struct BallContact {
     V3 reduction;
 };
 
+DI BallContact sel(bool c, const BallContact& a, const BallContact& b)
+{
+    return BallContact{ sel(c, a.point, b.point), sel(c, a.relPos, b.relPos), sel(c, a.normal, b.normal),
+                        sel(c, a.depth, b.depth), sel(c, a.reduction, b.reduction) };
+}
+
 // closest point on a triangle (Ericson, Real-Time Collision Detection 5.1.5)
 DI V3 closestOnTriangle(V3 p, V3 a, V3 b, V3 c)
 {
@@ -489,8 +508,8 @@ DI void adjustBallEdge(BallContact& ct, V3 t0, V3 t1, V3 t2, V3 angles)
         return;
     }
     const float side = angle > 0.f ? 1.f : -1.f;
-    const V3 s = bestEdge == 0 ? t0 : (bestEdge == 1 ? t1 : t2);
-    const V3 en = bestEdge == 0 ? t1 : (bestEdge == 1 ? t2 : t0);
+    const V3 s = sel(bestEdge == 0, t0, sel(bestEdge == 1, t1, t2));
+    const V3 en = sel(bestEdge == 0, t1, sel(bestEdge == 1, t2, t0));
     const V3 edgeAxis = normalize(en - s);
     const V3 nA = face * side;
     const V3 nB = rodrigues(face, edgeAxis, angle) * side;
@@ -514,89 +533,40 @@ DI void reduceBallContact(const Dev& d, V3 center, const Tri& t, BallContact* cs
     adjustBallEdge(ct, t.v0, t.v1, t.v2, V3{ ang.x, ang.y, ang.z });
     ct.point = (center + ct.relPos) + ct.normal * ct.depth;
 #pragma unroll
-    for (int i = 0; i < 4; i++)
-        if (i == slot) cs[i] = ct;
+    for (int i = 0; i < 4; i++) cs[i] = sel(i == slot, ct, cs[i]);
 }
 
-constexpr int kBallCandidates = 48;
-
-// Triangles of the overlapped cells, taken once each in ascending index order
-// (the reference merges the sorted cell lists, BallArena/Contact.cuh:513-594).
-// Fast path: collect the few triangles whose conservative AABB test passes,
-// sort them; if they do not fit, fall back to the k-way merge of the cells.
+// Sequential gather for a ball whose distinct contact triangles do not fit
+// the cooperative list (rare: only balls pressed into the goal-post mesh come
+// close): triangles of the overlapped cells in ascending index
+// order, taken once each (the reference merges the sorted cell lists,
+// BallArena/Contact.cuh:513-594).  Each pass finds the next larger triangle
+// index in contact, so no candidate array is kept.
 DI int gatherBallContacts(const Dev& d, V3 center, BallContact* cs)
 {
     const float ext = kBallRadius + kBallArenaBreak;
     int lo[3], hi[3];
     cellOf(center - ext, lo[0], lo[1], lo[2]);
     cellOf(center + ext, hi[0], hi[1], hi[2]);
-    const float reach = ext + 1.f;  // conservative: never rejects a real contact
-    int candRef[kBallCandidates], candIdx[kBallCandidates];
-    int nc = 0;
-    bool overflow = false;
-    for (int z = lo[2]; z <= hi[2] && !overflow; z++)
-        for (int y = lo[1]; y <= hi[1] && !overflow; y++)
-            for (int x = lo[0]; x <= hi[0] && !overflow; x++) {
-                const int cell = flatCell(x, y, z);
-                const int e = d.arena.cellStart[cell + 1];
-                for (int r = d.arena.cellStart[cell]; r < e; r++) {
-                    const Tri t = loadTri(d.arena, r);
-                    const V3 mn = vmin(vmin(t.v0, t.v1), t.v2);
-                    const V3 mx = vmax(vmax(t.v0, t.v1), t.v2);
-                    if (center.x < mn.x - reach || center.x > mx.x + reach || center.y < mn.y - reach ||
-                        center.y > mx.y + reach || center.z < mn.z - reach || center.z > mx.z + reach)
-                        continue;
-                    bool seen = false;  // a triangle registered in several cells is taken once
-                    for (int q = 0; q < nc; q++) seen |= candIdx[q] == t.idx;
-                    if (seen) continue;
-                    if (nc == kBallCandidates) { overflow = true; break; }
-                    candRef[nc] = r;
-                    candIdx[nc] = t.idx;
-                    nc++;
-                }
-            }
-    int count = 0;
-    if (!overflow) {
-        // insertion sort by triangle index
-        for (int i = 1; i < nc; i++) {
-            const int r = candRef[i], key = candIdx[i];
-            int j = i - 1;
-            while (j >= 0 && candIdx[j] > key) {
-                candRef[j + 1] = candRef[j];
-                candIdx[j + 1] = candIdx[j];
-                j--;
-            }
-            candRef[j + 1] = r;
-            candIdx[j + 1] = key;
-        }
-        for (int i = 0; i < nc; i++) reduceBallContact(d, center, loadTri(d.arena, candRef[i]), cs, count);
-        return count;
-    }
-    // slow path: k-way merge over the (at most 27) sorted cell runs
-    int cursor[27], end[27], cells = 0;
-    for (int z = lo[2]; z <= hi[2]; z++)
-        for (int y = lo[1]; y <= hi[1]; y++)
-            for (int x = lo[0]; x <= hi[0]; x++) {
-                const int cell = flatCell(x, y, z);
-                cursor[cells] = d.arena.cellStart[cell];
-                end[cells] = d.arena.cellStart[cell + 1];
-                cells++;
-            }
-    int last = -1;
+    int count = 0, last = -1;
     for (;;) {
-        int sel = -1, key = 0x7fffffff;
-        for (int c = 0; c < cells; c++) {
-            if (cursor[c] >= end[c]) continue;
-            const int idx = loadTri(d.arena, cursor[c]).idx;
-            if (idx < key) { key = idx; sel = c; }
-        }
-        if (sel < 0) break;
-        const int r = cursor[sel]++;
-        if (key == last) continue;
-        last = key;
-        reduceBallContact(d, center, loadTri(d.arena, r), cs, count);
+        int next = 0x7fffffff;
+        for (int z = lo[2]; z <= hi[2]; z++)
+            for (int y = lo[1]; y <= hi[1]; y++)
+                for (int x = lo[0]; x <= hi[0]; x++) {
+                    const int cell = flatCell(x, y, z);
+                    const int e = d.arena.cellStart[cell + 1];
+                    for (int r = d.arena.cellStart[cell]; r < e; r++) {
+                        const Tri t = loadTri(d.arena, r);
+                        if (t.idx <= last || t.idx >= next) continue;
+                        BallContact ct;
+                        if (sphereTriangle(center, t.v0, t.v1, t.v2, ct)) next = t.idx;
+                    }
+                }
+        if (next == 0x7fffffff) return count;
+        reduceBallContact(d, center, loadTriIdx(d.arena, next), cs, count);
+        last = next;
     }
-    return count;
 }
 
 // ---- cooperative gather: one wave gathers the arena contacts of 64 balls.
@@ -610,7 +580,7 @@ DI int gatherBallContacts(const Dev& d, V3 center, BallContact* cs)
 // order, which is exactly what the sequential merge produces: triangles that
 // fail the sphere test add nothing there either.
 constexpr int kBallCells = 12;  // a 186.3 uu box spans at most 3 x 2 x 2 cells
-constexpr int kBallHits = 64;  // distinct triangles within reach (about 50 at the goal posts)
+constexpr int kBallHits = 128;  // distinct triangles within reach (more than 64 seen at the goal posts)
 
 struct BallGatherLds {
     int excl[64];
@@ -1147,9 +1117,7 @@ DI void boostPads(const Dev& d, int s)
             }
             if (locked >= 0 && have < kBoostMax) {
                 const float next = fmin_(have + (big ? kBigPadAmount : kSmallPadAmount), kBoostMax);
-#pragma unroll
-                for (int k = 0; k < kMaxCars; k++)
-                    if (k == locked) boost[k] = next;
+                setAt(boost, locked, next);
                 changed |= 1 << locked;
                 cd = big ? kBigPadCooldown : kSmallPadCooldown;
             }

@@ -282,13 +282,26 @@ int carl_env_import_state(carl_env* env, const uint32_t* car_state,
                           const uint32_t* sim_state, int tick_count);
 
 /* ---- tick-kernel timing (no reference counterpart) -------------------------
- * With timing enabled, every tick-kernel launch is bracketed by a pair of HIP
- * events recorded on the environment stream.  carl_env_tick_timing
- * synchronises that stream, returns the summed launch duration (ms) and the
- * number of launches since timing was enabled or last read, and clears both.
- * Enabling or disabling also clears them. */
+ * One physics tick is five kernels on the environment stream, in this order
+ * (the reference's eleven per-tick launches, src/RLEnvironment.cu:166-211,
+ * grouped by the data they own). */
+enum {
+    CARL_KERNEL_CONTACT = 0,    /* broadphase, wheel rays, car-arena contact search */
+    CARL_KERNEL_CAR_ARENA = 1,  /* controls, suspension, car-arena solve */
+    CARL_KERNEL_CAR_CAR = 2,    /* episode clock, car-car pairs */
+    CARL_KERNEL_BALL = 3,       /* ball-arena, car-ball, goal */
+    CARL_KERNEL_FINISH = 4,     /* integration, impulse caches, boost pads */
+    CARL_TICK_KERNELS = 5
+};
+
+/* With timing enabled, HIP events recorded on the environment stream bracket
+ * every tick kernel.  carl_env_tick_timing synchronises that stream and
+ * returns, per kernel (arrays of CARL_TICK_KERNELS), the summed duration in
+ * ms and the launch count since timing was enabled or last read, then clears
+ * them.  Enabling or disabling also clears them. */
 int carl_env_enable_timing(carl_env* env, int enable);
-int carl_env_tick_timing(carl_env* env, double* total_ms, int* launches);
+int carl_env_tick_timing(carl_env* env, double* kernel_ms, int* launches);
+const char* carl_tick_kernel_name(int kernel);
 
 /* ---- primitives ------------------------------------------------------------ */
 
