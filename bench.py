@@ -100,6 +100,8 @@ def main() -> None:
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-ticks", type=int, default=1_200_000,
                     help="CPU-baseline ticks per host thread (0 skips it)")
+    ap.add_argument("--tick-streams", type=int, default=0,
+                    help="partitions of the simulations ticked on separate streams (0: engine default)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (HBM counter calibration) and exit")
     args = ap.parse_args()
@@ -130,6 +132,8 @@ def main() -> None:
     rng = np.random.default_rng(args.seed)
     env = carl_amd.Env(n_sim, args.blue, args.orange, args.seed, args.tick_skip, True, False, False)
     stream = torch.cuda.ExternalStream(env.stream, device=dev)
+    if args.tick_streams:
+        env.tick_streams = args.tick_streams
 
     odd = np.arange(1, n_sim, 2)
     reset = workloads.random_reset_state(rng, len(odd), n_cars)

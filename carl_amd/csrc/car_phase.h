@@ -603,6 +603,16 @@ DI void satAxis(V3 ax, const LocalTri& t, int idx, bool norm, Sat& s)
 
 DI Sat boxTriSat(const LocalTri& t)
 {
+    // The box face axes first, as a pure rejection: the overlap verdict is the
+    // conjunction over all axes, so testing three of them early changes
+    // nothing, and they are cheap (no normalisation); most cell triangles
+    // miss the box along one of them.  The bookkeeping pass below then runs
+    // every axis in the reference order.
+    Sat pre{ true, 0, kFltMax, kZero };
+    satAxis(kX, t, 1, false, pre);
+    satAxis(kY, t, 2, false, pre);
+    satAxis(kZ, t, 3, false, pre);
+    if (!pre.overlap) return pre;
     Sat s{ true, 0, kFltMax, kZero };
     satAxis(cross(t.e0, t.e1), t, 0, true, s);
     if (!s.overlap) return s;
@@ -943,9 +953,15 @@ struct ContactLds {
 
 constexpr unsigned long long kNoKey = ~0ull;
 
-DI void contactItem(const Dev& d, ContactLds& L, int o, int q, int base, int lane)
+// the cell triangle of item q of owner o (a dummy load of reference 0 for
+// lanes without an item keeps the pipeline uniform)
+DI Tri contactFetch(const Dev& d, const ContactLds& L, int o, int q, bool valid)
 {
-    const Tri t = loadTri(d.arena, L.first[o] + q);
+    return loadTri(d.arena, valid ? L.first[o] + q : 0);
+}
+
+DI void contactItem(const Dev& d, ContactLds& L, const Tri& t, int o, int q, int base, int lane)
+{
     const V3 dir{ L.dir[0][o], L.dir[1][o], L.dir[2][o] };
     const V3 pv = cross(dir, t.e2);
     const float det = dot(t.e1, pv);

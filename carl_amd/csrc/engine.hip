@@ -47,23 +47,35 @@ int fail(int code, const std::string& msg)
 // ------------------------------------------------------------------ kernels
 
 constexpr int kTickBlock = 256;
+constexpr int kMaxTickStreams = 4;
 
 // Per-tick car workspace between the contact and the car-arena kernels, one
 // plane of nTotal 32-bit words each: wheel hit distance, normal xyz and
 // source per wheel, then the cell reference of the deepest arena contact.
 enum : int { kWsDist = 0, kWsNx = 4, kWsNy = 8, kWsNz = 12, kWsSrc = 16, kWsBest = 20, kWsPlanes = 21 };
 
+// Simulations [begin, end) of one launch: the tick runs as independent
+// partitions on separate streams so the tail of one partition's kernel
+// overlaps the next kernel of the other.
+struct SimRange {
+    int begin, end;
+};
+
 // A1: broadphase, suspension raycast and car-arena contact search of every
 // car against the pre-tick poses of the arena, the other cars and the ball.
-// One wave per block; the cell runs of its 64 cars are searched together.
+// One wave per block; the cell runs of its kContactOwners cars are searched
+// by all 64 lanes together.  Fewer owners than lanes spreads the search over
+// more waves: the work is latency-bound and 65536 1v1 simulations would
+// otherwise leave two waves per SIMD.
 constexpr int kContactBlock = 64;
+constexpr int kContactOwners = 32;
 
-__global__ __launch_bounds__(kContactBlock) void contactKernel(Dev d, uint32_t* __restrict__ ws)
+__global__ __launch_bounds__(kContactBlock) void contactKernel(Dev d, uint32_t* __restrict__ ws, SimRange range)
 {
     __shared__ ContactLds L;
     const int lane = threadIdx.x;
-    const int car = blockIdx.x * kContactBlock + lane;
-    const bool ok = car < d.nTotal;
+    const int car = range.begin * d.nCars + blockIdx.x * kContactOwners + lane;
+    const bool ok = lane < kContactOwners && car < range.end * d.nCars;
     V3 cen = kZero;
     Q4 rot{ 0.f, 0.f, 0.f, 1.f };
     Broad bp{ 0, 0 };
@@ -76,7 +88,9 @@ __global__ __launch_bounds__(kContactBlock) void contactKernel(Dev d, uint32_t* 
     }
     contactPrepare(L, lane, ok && !demoed, cen, rot, bp.start);
     __syncthreads();
-    waveItems(bp.count, L.excl, [&](int o, int q, int base) { contactItem(d, L, o, q, base, lane); });
+    waveItemsPipelined(
+        bp.count, L.excl, [&](int o, int q, bool valid) { return contactFetch(d, L, o, q, valid); },
+        [&](const Tri& t, int o, int q, int base) { contactItem(d, L, t, o, q, base, lane); });
     __syncthreads();
     if (!ok) return;
     Wheels w;
@@ -96,10 +110,11 @@ __global__ __launch_bounds__(kContactBlock) void contactKernel(Dev d, uint32_t* 
 // A2: controls, car-arena contacts, suspension and the contact solve.
 // two waves per SIMD keep all of its waves resident at 65536 1v1 simulations
 __global__ __launch_bounds__(kTickBlock, 2) void carArenaKernel(Dev d, const uint32_t* __restrict__ ws, int kind,
-                                                             const void* __restrict__ actions, int tick)
+                                                             const void* __restrict__ actions, int tick,
+                                                             SimRange range)
 {
-    const int car = blockIdx.x * kTickBlock + threadIdx.x;
-    if (car >= d.nTotal) return;
+    const int car = range.begin * d.nCars + blockIdx.x * kTickBlock + threadIdx.x;
+    if (car >= range.end * d.nCars) return;
     const size_t n = d.nTotal;
     Wheels w;
 #pragma unroll
@@ -130,10 +145,10 @@ __global__ __launch_bounds__(kTickBlock, 2) void carArenaKernel(Dev d, const uin
 
 // B1: episode clock and the car-car pairs of each simulation, (b, a) with b
 // the later car.
-__global__ __launch_bounds__(kTickBlock) void carCarKernel(Dev d, int tick)
+__global__ __launch_bounds__(kTickBlock) void carCarKernel(Dev d, int tick, SimRange range)
 {
-    const int sim = blockIdx.x * kTickBlock + threadIdx.x;
-    if (sim >= d.nSim) return;
+    const int sim = range.begin + blockIdx.x * kTickBlock + threadIdx.x;
+    if (sim >= range.end) return;
     d.sseti(CARL_SIM_EPISODE_TICKS, sim, d.si(CARL_SIM_EPISODE_TICKS, sim) + 1);
     const int base = sim * d.nCars;
     for (int a = 0; a < d.nCars - 1; a++)
@@ -141,15 +156,17 @@ __global__ __launch_bounds__(kTickBlock) void carCarKernel(Dev d, int tick)
 }
 
 // B2: ball-arena contacts, car-ball pairs and goal detection.  One wave per
-// block; the arena contacts of its 64 balls are gathered cooperatively.
+// block; the arena contacts of its kBallOwners balls are gathered by all 64
+// lanes cooperatively.
 constexpr int kBallBlock = 64;
+constexpr int kBallOwners = 32;
 
-__global__ __launch_bounds__(kBallBlock) void ballKernel(Dev d, int tick)
+__global__ __launch_bounds__(kBallBlock) void ballKernel(Dev d, int tick, SimRange range)
 {
     __shared__ BallGatherLds L;
     const int lane = threadIdx.x;
-    const int sim = blockIdx.x * kBallBlock + lane;
-    const bool ok = sim < d.nSim;
+    const int sim = range.begin + blockIdx.x * kBallOwners + lane;
+    const bool ok = lane < kBallOwners && sim < range.end;
     const bool awake = ok && !ballSleeping(d, sim);
     const V3 center = ok ? d.sv(CARL_SIM_BALL_POS, sim) : kZero;
     int items = 0;
@@ -167,7 +184,9 @@ __global__ __launch_bounds__(kBallBlock) void ballKernel(Dev d, int tick)
     L.hitN[lane] = 0;
     if (!awake || sequential) L.runs[lane] = 0;
     __syncthreads();
-    waveItems(items, L.excl, [&](int o, int q, int) { ballGatherItem(d, L, o, q); });
+    waveItemsPipelined(
+        items, L.excl, [&](int o, int q, bool valid) { return ballGatherFetch(d, L, o, q, valid); },
+        [&](const BallItem& item, int o, int, int) { ballGatherItem(L, item, o); });
     __syncthreads();
     if (!ok) return;
     BallContact cs[4];
@@ -182,15 +201,15 @@ __global__ __launch_bounds__(kBallBlock) void ballKernel(Dev d, int tick)
 // C + D: integration and impulse caches of every car and ball, then the
 // boost pads of each simulation once all of its cars have moved.  A block
 // owns whole simulations (simsPerBlock * nCars car lanes).
-__global__ __launch_bounds__(kTickBlock) void finishKernel(Dev d, int simsPerBlock)
+__global__ __launch_bounds__(kTickBlock) void finishKernel(Dev d, int simsPerBlock, SimRange range)
 {
     const int t = threadIdx.x;
-    const int simBase = blockIdx.x * simsPerBlock;
+    const int simBase = range.begin + blockIdx.x * simsPerBlock;
     const int mySim = simBase + t / d.nCars;
     const int car = mySim * d.nCars + t % d.nCars;
     const int laneSim = simBase + t;
-    if (t < simsPerBlock * d.nCars && mySim < d.nSim) finishCar(d, car);
-    const bool simOk = t < simsPerBlock && laneSim < d.nSim;
+    if (t < simsPerBlock * d.nCars && mySim < range.end) finishCar(d, car);
+    const bool simOk = t < simsPerBlock && laneSim < range.end;
     if (simOk) finishBall(d, laneSim);
     __syncthreads();
     if (simOk) boostPads(d, laneSim);
@@ -291,7 +310,9 @@ __global__ __launch_bounds__(kContactBlock) void refreshKernel(Dev d, Selection 
     }
     contactPrepare(L, lane, false, cen, rot, bp.start);
     __syncthreads();
-    waveItems(bp.count, L.excl, [&](int o, int q, int base) { contactItem(d, L, o, q, base, lane); });
+    waveItemsPipelined(
+        bp.count, L.excl, [&](int o, int q, bool valid) { return contactFetch(d, L, o, q, valid); },
+        [&](const Tri& t, int o, int q, int base) { contactItem(d, L, t, o, q, base, lane); });
     __syncthreads();
     if (car < 0) return;
     if (!active) {
@@ -423,6 +444,9 @@ struct carl_env {
     int32_t* actions = nullptr;
     float* cactions = nullptr;
     uint32_t* ws = nullptr;  // per-tick car workspace (kWsPlanes planes)
+    int tickStreams = kMaxTickStreams;   // partitions of the tick, one stream each
+    hipStream_t aux[kMaxTickStreams - 1] = {};
+    hipEvent_t fork = nullptr, join[kMaxTickStreams - 1] = {};
     bool timing = false;
     // timing markers: per timed tick, one event before each tick kernel and
     // one after the last (CARL_TICK_KERNELS + 1); reusable pool
@@ -458,6 +482,11 @@ void freeAll(carl_env* e)
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
     for (hipEvent_t ev : e->marks) (void)hipEventDestroy(ev);
+    for (int i = 0; i < kMaxTickStreams - 1; i++) {
+        if (e->join[i]) (void)hipEventDestroy(e->join[i]);
+        if (e->aux[i]) (void)hipStreamDestroy(e->aux[i]);
+    }
+    if (e->fork) (void)hipEventDestroy(e->fork);
     if (e->stream) (void)hipStreamDestroy(e->stream);
 }
 
@@ -483,29 +512,52 @@ int mark(carl_env* e, int i)
         if (rc_ != CARL_OK) return rc_;   \
     } while (0)
 
+// Ticks run as e->tickStreams partitions of the simulations, partition 0 on
+// the environment stream and the others on auxiliary streams forked from and
+// joined back into it; the partitions share no data within a tick.  Timing
+// markers bracket partition 0's kernels.
 int launchTicks(carl_env* e, int kind, const void* actions, int n)
 {
     if (n <= 0) return CARL_OK;
     const int spb = kTickBlock / e->nCars;
-    const int blocks = (e->nSim + spb - 1) / spb;
     const Dev d = e->dev();
-    const int carBlocks = e->grid(e->nTotal, kTickBlock), simBlocks = e->grid(e->nSim, kTickBlock);
+    const int parts = std::min(e->tickStreams, e->nSim);
+    SimRange range[kMaxTickStreams];
+    hipStream_t stream[kMaxTickStreams];
+    for (int p = 0; p < parts; p++) {
+        range[p] = SimRange{ (int)((int64_t)e->nSim * p / parts), (int)((int64_t)e->nSim * (p + 1) / parts) };
+        stream[p] = p == 0 ? e->stream : e->aux[p - 1];
+    }
+    if (parts > 1) {
+        HIP_TRY(hipEventRecord(e->fork, e->stream));
+        for (int p = 1; p < parts; p++) HIP_TRY(hipStreamWaitEvent(stream[p], e->fork, 0));
+    }
     for (int k = 0; k < n; k++) {
         const int tick = e->tickCount + k + 1;
-        CARL_MARK(CARL_KERNEL_CONTACT);
-        contactKernel<<<e->grid(e->nTotal, kContactBlock), kContactBlock, 0, e->stream>>>(d, e->ws);
-        CARL_MARK(CARL_KERNEL_CAR_ARENA);
-        carArenaKernel<<<carBlocks, kTickBlock, 0, e->stream>>>(d, e->ws, kind, actions, tick);
-        CARL_MARK(CARL_KERNEL_CAR_CAR);
-        carCarKernel<<<simBlocks, kTickBlock, 0, e->stream>>>(d, tick);
-        CARL_MARK(CARL_KERNEL_BALL);
-        ballKernel<<<e->grid(e->nSim, kBallBlock), kBallBlock, 0, e->stream>>>(d, tick);
-        CARL_MARK(CARL_KERNEL_FINISH);
-        finishKernel<<<blocks, spb * e->nCars, 0, e->stream>>>(d, spb);
-        CARL_MARK(CARL_TICK_KERNELS);
+        for (int p = 0; p < parts; p++) {
+            const SimRange r = range[p];
+            const int sims = r.end - r.begin, cars = sims * e->nCars;
+            hipStream_t st = stream[p];
+            const bool timed = p == 0;
+            if (timed) CARL_MARK(CARL_KERNEL_CONTACT);
+            contactKernel<<<e->grid(cars, kContactOwners), kContactBlock, 0, st>>>(d, e->ws, r);
+            if (timed) CARL_MARK(CARL_KERNEL_CAR_ARENA);
+            carArenaKernel<<<e->grid(cars, kTickBlock), kTickBlock, 0, st>>>(d, e->ws, kind, actions, tick, r);
+            if (timed) CARL_MARK(CARL_KERNEL_CAR_CAR);
+            carCarKernel<<<e->grid(sims, kTickBlock), kTickBlock, 0, st>>>(d, tick, r);
+            if (timed) CARL_MARK(CARL_KERNEL_BALL);
+            ballKernel<<<e->grid(sims, kBallOwners), kBallBlock, 0, st>>>(d, tick, r);
+            if (timed) CARL_MARK(CARL_KERNEL_FINISH);
+            finishKernel<<<e->grid(sims, spb), spb * e->nCars, 0, st>>>(d, spb, r);
+            if (timed) CARL_MARK(CARL_TICK_KERNELS);
+        }
         if (e->timing) e->timedTicks++;
     }
     HIP_TRY(hipGetLastError());
+    for (int p = 1; p < parts; p++) {
+        HIP_TRY(hipEventRecord(e->join[p - 1], stream[p]));
+        HIP_TRY(hipStreamWaitEvent(e->stream, e->join[p - 1], 0));
+    }
     e->tickCount += n;
     return CARL_OK;
 }
@@ -657,6 +709,13 @@ int carl_env_create(int nSim, int nBlue, int nOrange, int seed, int frameskip, i
     };
     if (hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking) != hipSuccess)
         return bail(fail(CARL_ERR_RUNTIME, "hipStreamCreate failed"));
+    if (hipEventCreateWithFlags(&e->fork, hipEventDisableTiming) != hipSuccess)
+        return bail(fail(CARL_ERR_RUNTIME, "hipEventCreate failed"));
+    for (int i = 0; i < kMaxTickStreams - 1; i++) {
+        if (hipStreamCreateWithFlags(&e->aux[i], hipStreamNonBlocking) != hipSuccess
+            || hipEventCreateWithFlags(&e->join[i], hipEventDisableTiming) != hipSuccess)
+            return bail(fail(CARL_ERR_RUNTIME, "hipStreamCreate failed"));
+    }
     const size_t nT = (size_t)e->nTotal, nS = (size_t)nSim;
     int rc = CARL_OK;
     rc = rc ? rc : devAlloc(&e->car, (size_t)CARL_CAR_FIELDS * nT);
@@ -886,6 +945,10 @@ int carl_env_set_param(carl_env* e, int p, int v)
         if (v < 1) return fail(CARL_ERR_VALUE, "frameskip must be at least 1");
         e->frameskip = v;
         return CARL_OK;
+    case CARL_PARAM_TICK_STREAMS:
+        if (v < 1 || v > kMaxTickStreams) return fail(CARL_ERR_VALUE, "tick_streams must be in [1, 4]");
+        e->tickStreams = v;
+        return CARL_OK;
     default: return fail(CARL_ERR_VALUE, "parameter is read-only or unknown");
     }
 }
@@ -906,6 +969,7 @@ int carl_env_get_param(carl_env* e, int p, int* v)
     case CARL_PARAM_STATE_DIM: *v = e->stateDim; break;
     case CARL_PARAM_TICK_COUNT: *v = e->tickCount; break;
     case CARL_PARAM_N_BLUE: *v = e->nBlue; break;
+    case CARL_PARAM_TICK_STREAMS: *v = e->tickStreams; break;
     default: return fail(CARL_ERR_VALUE, "unknown parameter");
     }
     return CARL_OK;

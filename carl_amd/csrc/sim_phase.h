@@ -623,13 +623,27 @@ DI int ballGatherRuns(const Dev& d, V3 center, BallGatherLds& L, int lane)
     return count;
 }
 
-DI void ballGatherItem(const Dev& d, BallGatherLds& L, int o, int q)
+struct BallItem {
+    Tri t;
+    int run;  // which of the owner's cell runs the triangle came from
+};
+
+// the triangle of item q of owner o (reference 0 for lanes without an item)
+DI BallItem ballGatherFetch(const Dev& d, const BallGatherLds& L, int o, int q, bool valid)
 {
-    const int nr = L.runs[o];
-    int r = 0;
-    while (r + 1 < nr && L.runFirst[r + 1][o] <= q) r++;
-    const int ref = L.runStart[r][o] + (q - L.runFirst[r][o]);
-    const Tri t = loadTri(d.arena, ref);
+    int r = 0, ref = 0;
+    if (valid) {
+        const int nr = L.runs[o];
+        while (r + 1 < nr && L.runFirst[r + 1][o] <= q) r++;
+        ref = L.runStart[r][o] + (q - L.runFirst[r][o]);
+    }
+    return BallItem{ loadTri(d.arena, ref), r };
+}
+
+DI void ballGatherItem(BallGatherLds& L, const BallItem& item, int o)
+{
+    const Tri& t = item.t;
+    const int r = item.run;
     const V3 center{ L.cx[o], L.cy[o], L.cz[o] };
     const float reach = kBallRadius + kBallArenaBreak + 1.f;
     const V3 mn = vmin(vmin(t.v0, t.v1), t.v2);

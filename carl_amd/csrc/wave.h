@@ -54,4 +54,47 @@ __device__ __forceinline__ void waveItems(int count, int* excl, Body&& body)
     }
 }
 
+// waveItems with a two-stage pipeline: fetch(owner, item) issues the loads of
+// the next round before process(value, owner, item, base) runs on the current
+// one, so each round's memory latency overlaps the previous round's work.
+// Same visiting order and lane placement as waveItems.
+template <typename Fetch, typename Process>
+__device__ __forceinline__ void waveItemsPipelined(int count, int* excl, Fetch&& fetch, Process&& process)
+{
+    const int lane = (int)(threadIdx.x & 63);
+    const int incl = waveInclusiveScan(count);
+    const int total = __builtin_amdgcn_readlane(incl, 63);
+    excl[lane] = incl - count;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    auto owner = [&](int j) {
+        int o = 0;
+#pragma unroll
+        for (int step = 32; step > 0; step >>= 1)
+            if (excl[o + step] <= j) o += step;
+        return o;
+    };
+    if (total == 0) return;
+    int o = 0, q = 0;
+    if (lane < total) {
+        o = owner(lane);
+        q = lane - excl[o];
+    }
+    auto cur = fetch(o, q, lane < total);
+    for (int base = 0; base < total; base += 64) {
+        const int jn = base + 64 + lane;
+        int on = 0, qn = 0;
+        if (jn < total) {
+            on = owner(jn);
+            qn = jn - excl[on];
+        }
+        auto next = fetch(on, qn, jn < total);
+        if (base + lane < total) process(cur, o, q, base);
+        cur = next;
+        o = on;
+        q = qn;
+    }
+}
+
 }  // namespace carl

@@ -107,7 +107,9 @@ enum {
     CARL_PARAM_ACT_DIM = 7,      /* read-only */
     CARL_PARAM_STATE_DIM = 8,    /* read-only */
     CARL_PARAM_TICK_COUNT = 9,   /* read-only: global physics tick counter */
-    CARL_PARAM_N_BLUE = 10       /* read-only */
+    CARL_PARAM_N_BLUE = 10,      /* read-only */
+    CARL_PARAM_TICK_STREAMS = 11 /* partitions of the simulations, each ticked on its own stream [1, 4];
+                                    no reference counterpart (default 4) */
 };
 
 /* ---- persistent state layout (export / import) ------------------------

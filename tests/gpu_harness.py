@@ -122,3 +122,33 @@ class Pair:
         """Copy the engine's persistent state into the oracle."""
         car, sim, tick = gpu_state(self.gpu)
         self.cpu.import_state(car, sim, tick)
+
+
+def dense_geometry_reset_state(rng: np.random.Generator, n_rows: int, n_cars: int) -> dict[str, np.ndarray]:
+    """Reset inputs that put cars and balls where the arena mesh is densest:
+    corner ramps, goal mouths and posts, side walls (car on the wall) and the
+    ceiling, with velocities pointing into the geometry."""
+    spots = np.array([[3900.0, 4950.0, 60.0], [-3900.0, -4950.0, 60.0], [890.0, 5100.0, 100.0],
+                      [-890.0, -5100.0, 300.0], [0.0, 5300.0, 200.0], [4050.0, 0.0, 300.0],
+                      [-4050.0, 1000.0, 600.0], [2000.0, -3000.0, 1980.0], [3500.0, -4600.0, 200.0]])
+    pick = rng.integers(0, len(spots), (n_rows, n_cars))
+    car_pos = spots[pick] + rng.uniform(-60, 60, (n_rows, n_cars, 3))
+    axis = rng.normal(size=(n_rows, n_cars, 3))
+    axis /= np.linalg.norm(axis, axis=-1, keepdims=True)
+    ang = rng.uniform(-np.pi, np.pi, (n_rows, n_cars, 1))
+    rot = np.concatenate([axis * np.sin(ang / 2), np.cos(ang / 2)], axis=-1)
+    toward = -car_pos / np.maximum(np.linalg.norm(car_pos, axis=-1, keepdims=True), 1.0)
+    car_vel = -toward * rng.uniform(0, 1500, (n_rows, n_cars, 1))     # into the wall
+    bpick = rng.integers(0, len(spots), n_rows)
+    ball_pos = spots[bpick] + rng.uniform(-80, 80, (n_rows, 3))
+    ball_pos[:, 2] = np.maximum(ball_pos[:, 2], 95.0)
+    ball_vel = rng.normal(size=(n_rows, 3)) * 800.0
+    f32 = lambda x: np.ascontiguousarray(x, dtype=np.float32)  # noqa: E731
+    return {
+        "ball_position": f32(ball_pos), "ball_velocity": f32(ball_vel),
+        "ball_angular_velocity": f32(rng.normal(size=(n_rows, 3))),
+        "car_position": f32(car_pos), "car_rotation": f32(rot), "car_velocity": f32(car_vel),
+        "car_angular_velocity": f32(rng.normal(size=(n_rows, n_cars, 3))),
+        "car_demoed": np.zeros((n_rows, n_cars), dtype=np.bool_),
+        "car_boost": f32(rng.uniform(0, 100, (n_rows, n_cars))),
+    }

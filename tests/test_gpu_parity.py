@@ -14,7 +14,7 @@ import pytest
 import torch
 
 from carl_amd import workloads
-from gpu_harness import Pair, dev, gpu_state
+from gpu_harness import Pair, dense_geometry_reset_state, dev, gpu_state
 
 pytestmark = pytest.mark.gpu
 
@@ -105,6 +105,22 @@ def test_clustered_3v3_contacts(gpu):
         _assert_clean(p.state_mismatches(), f"state after step {step}")
         _assert_clean(p.output_mismatches(), f"outputs after step {step}")
     p.close()
+
+
+def test_dense_geometry_1v1_and_3v3(gpu):
+    """Cars and balls in corners, goal mouths, on posts, walls and the ceiling:
+    long cell runs, many SAT hits and large ball contact lists."""
+    rng = np.random.default_rng(14)
+    for n_blue, n, steps in ((1, 128, 20), (3, 32, 12)):
+        nc = 2 * n_blue
+        p = Pair(n, n_blue, n_blue, seed=8, frameskip=4)
+        p.apply_reset_state(dense_geometry_reset_state(rng, n, nc))
+        _assert_clean(p.state_mismatches(), f"{n_blue}v{n_blue} state after dense reset")
+        for step in range(steps):
+            p.step_continuous(workloads.random_continuous_actions(rng, n, nc))
+            _assert_clean(p.state_mismatches(), f"{n_blue}v{n_blue} state after step {step}")
+            _assert_clean(p.output_mismatches(), f"{n_blue}v{n_blue} outputs after step {step}")
+        p.close()
 
 
 def test_2v2_masked_resets_every_step(gpu):
