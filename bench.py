@@ -68,6 +68,22 @@ def kernel_bytes(kernel: str, n_cars: int) -> int:
     return 4 * words
 
 
+TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_1v1_n65536_ts8.md"
+
+
+def measured_traffic(kernel: str, n_sim: int, n_cars: int, tick_skip: int, parts: int):
+    """HBM bytes per dispatch of `kernel` from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary of the headline workload (copy-calibrated);
+    None for any other workload or when the summary is absent."""
+    if (n_sim, n_cars, tick_skip, parts) != (65536, 2, 8, 4) or not TRAFFIC_FILE.is_file():
+        return None
+    for line in TRAFFIC_FILE.read_text().splitlines():
+        f = line.split()
+        if len(f) == 3 and f[0] == "traffic" and f[1] == kernel:
+            return int(f[2])
+    return None
+
+
 def cpu_baseline(ticks_per_thread: int, seed: int) -> dict:
     import ctypes
 
@@ -170,7 +186,11 @@ def main() -> None:
     kernel = max(timing, key=lambda k: timing[k][0])
     kernel_ms, launches = timing[kernel]
     launch_ms = kernel_ms / launches
-    launch_bytes = kernel_bytes(kernel, n_cars) * n_sim
+    # each launch covers one partition of the simulations; the engine times
+    # partition 0, which holds n_sim // tick_streams of them
+    parts = min(env.tick_streams, n_sim)
+    launch_sims = n_sim // parts
+    launch_bytes = kernel_bytes(kernel, n_cars) * launch_sims
     achieved = launch_bytes / (launch_ms * 1e-3) / 1e9
     tick_ms = sum(ms for ms, _ in timing.values())
 
@@ -196,6 +216,7 @@ def main() -> None:
             "n_cars": n_cars,
             "tick_skip": args.tick_skip,
             "parallelism": "single GPU",
+            "tick_streams": parts,
         },
         "roofline": {
             "bound": "hbm",
@@ -204,10 +225,12 @@ def main() -> None:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": None,
+            "traffic": measured_traffic(kernel, n_sim, n_cars, args.tick_skip, parts),
+            "traffic_source": TRAFFIC_FILE.name,
             "launch_ms": launch_ms,
             "launches": launches,
             "bytes_per_launch": launch_bytes,
+            "sims_per_launch": launch_sims,
         },
         "tick_kernels_ms_per_launch": {k: ms / n for k, (ms, n) in timing.items()},
         "tick_pipeline": {

@@ -74,6 +74,10 @@ void oracle_probe_autoflip(const float* quat, int jump, int contacts, const floa
                            int* is_auto_flipping, float* timer, float* ang);
 void oracle_probe_steer_stage(float staged, float* prev_out, float* cur_out);
 int oracle_kickoff_perm(int idx, int slot);
+/* SAT probes: triangle in box-local coordinates; two car hitboxes in world */
+void oracle_probe_box_tri_sat(const float* tri, int* overlap, int* axis_idx, float* depth, float* axis);
+void oracle_probe_box_box_sat(const float* cen_a, const float* rot_a, const float* cen_b, const float* rot_b,
+                              int* overlap, int* axis_idx, float* depth);
 uint32_t oracle_hash32(uint32_t v);
 void oracle_sincos(float x, float* s, float* c);
 float oracle_atan2(float y, float x);

@@ -776,6 +776,12 @@ void oracle_probe_autoflip(const float* q, int j, int n, const float* nrm, int* 
 }
 void oracle_probe_steer_stage(float s, float* p, float* c) { ophys_probe_steer_stage(s, p, c); }
 int oracle_kickoff_perm(int i, int s) { return ophys_kickoff_perm(i, s); }
+void oracle_probe_box_tri_sat(const float* t, int* o, int* a, float* d, float* ax) { ophys_probe_box_tri_sat(t, o, a, d, ax); }
+void oracle_probe_box_box_sat(const float* ca, const float* ra, const float* cb, const float* rb, int* o, int* a,
+                              float* d)
+{
+    ophys_probe_box_box_sat(ca, ra, cb, rb, o, a, d);
+}
 uint32_t oracle_hash32(uint32_t v) { return o_hash32(v); }
 void oracle_sincos(float x, float* s, float* c) { o_sincos(x, s, c); }
 float oracle_atan2(float y, float x) { return o_atan2(y, x); }

@@ -310,6 +310,9 @@ void ophys_init_empty_wheels(OCar* c, V3 up);
 Q4 ophys_integrate_quat(Q4 rot, V3 ang);
 void ophys_controls_decode(int kind, const void* actions, int car, OControls* out);
 int ophys_kickoff_perm(int idx, int slot);
+void ophys_probe_box_tri_sat(const float* tri, int* overlap, int* axisIdx, float* depth, float* axis);
+void ophys_probe_box_box_sat(const float* cenA, const float* rotA, const float* cenB, const float* rotB,
+                             int* overlap, int* axisIdx, float* depth);
 V3 ophys_pad_pos(int pad);
 int ophys_ball_hit_prev_tick(int hitTick, int tick);
 

@@ -2466,3 +2466,28 @@ void ophys_probe_steer_stage(float staged, float* prevOut, float* curOut)
     *prevOut = c->steerPrev;
     *curOut = c->steer;
 }
+
+/* box-triangle SAT of a triangle given in box-local coordinates (SAT.cuh:42-121) */
+void ophys_probe_box_tri_sat(const float* tri, int* overlap, int* axisIdx, float* depth, float* axis)
+{
+    OTri t;
+    tri_set(&t, v3(tri[0], tri[1], tri[2]), v3(tri[3], tri[4], tri[5]), v3(tri[6], tri[7], tri[8]));
+    t.delta = vneg(tri_center(&t));
+    const OSat s = tri_sat(&t);
+    *overlap = s.overlap;
+    *axisIdx = s.axisIdx;
+    *depth = s.minPen;
+    axis[0] = s.minAxis.x; axis[1] = s.minAxis.y; axis[2] = s.minAxis.z;
+}
+
+/* box-box SAT of two car hitboxes (CarCar/SAT.cuh:46-125) */
+void ophys_probe_box_box_sat(const float* cenA, const float* rotA, const float* cenB, const float* rotB,
+                             int* overlap, int* axisIdx, float* depth)
+{
+    const OBox A = { v3(cenA[0], cenA[1], cenA[2]), q4(rotA[0], rotA[1], rotA[2], rotA[3]) };
+    const OBox B = { v3(cenB[0], cenB[1], cenB[2]), q4(rotB[0], rotB[1], rotB[2], rotB[3]) };
+    const OSat s = cc_sat(&A, &B);
+    *overlap = s.overlap;
+    *axisIdx = s.axisIdx;
+    *depth = s.minPen;
+}

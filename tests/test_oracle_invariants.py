@@ -204,3 +204,161 @@ def test_quaternion_integration_keeps_unit_norm():
         assert abs(np.linalg.norm(r) - 1.0) < 1e-6
         # small rotation: the result is close to q rotated by |w| dt
         assert abs(abs(float(r @ q)) - math.cos(np.linalg.norm(w) * DT / 2)) < 1e-5
+
+
+# ---------------------------------------------------------------- SAT by linear programming
+
+HALF = np.array([60.186455, 43.282655, 19.262505])
+
+
+def _lp_margin(A_ub, b_ub, A_eq=None, b_eq=None, n_free=0, n_pos=0):
+    """max s subject to A_ub [x, s] <= b_ub (x: n_free free then n_pos >= 0)."""
+    from scipy.optimize import linprog
+
+    n = n_free + n_pos + 1
+    c = np.zeros(n)
+    c[-1] = -1.0
+    bounds = [(None, None)] * n_free + [(0, None)] * n_pos + [(None, None)]
+    r = linprog(c, A_ub=A_ub, b_ub=b_ub, A_eq=A_eq, b_eq=b_eq, bounds=bounds, method="highs")
+    assert r.status == 0
+    return -r.fun
+
+
+def box_tri_margin(tri):
+    """Largest s with a point of the triangle inside the box shrunk by s (s < 0: disjoint)."""
+    A, b = [], []
+    for k in range(3):
+        for sgn in (1.0, -1.0):
+            A.append([sgn * tri[i][k] for i in range(3)] + [1.0])
+            b.append(HALF[k])
+    return _lp_margin(np.array(A), np.array(b), A_eq=np.array([[1.0, 1.0, 1.0, 0.0]]), b_eq=[1.0], n_pos=3)
+
+
+def _rot(q):
+    x, y, z, w = q
+    return np.array([[1 - 2 * (y * y + z * z), 2 * (x * y - w * z), 2 * (x * z + w * y)],
+                     [2 * (x * y + w * z), 1 - 2 * (x * x + z * z), 2 * (y * z - w * x)],
+                     [2 * (x * z - w * y), 2 * (y * z + w * x), 1 - 2 * (x * x + y * y)]])
+
+
+def box_box_margin(ca, qa, cb, qb):
+    A, b = [], []
+    for c, q in ((ca, qa), (cb, qb)):
+        R = _rot(q)
+        for k in range(3):
+            for sgn in (1.0, -1.0):
+                A.append(list(sgn * R[:, k]) + [1.0])
+                b.append(HALF[k] + sgn * R[:, k] @ c)
+    return _lp_margin(np.array(A), np.array(b), n_free=3)
+
+
+def test_box_triangle_sat_agrees_with_linear_programming():
+    """The 13-axis SAT verdict equals the LP feasibility of a common point, and
+    moving the triangle by the reported depth along the reported axis (one of
+    its two senses) separates the pair."""
+    rng = np.random.default_rng(5)
+    ov, ax, dp = C.c_int(), C.c_int(), F()
+    axis = (F * 3)()
+    checked = hits = 0
+    for _ in range(600):
+        centre = rng.normal(size=3) * np.array([70.0, 50.0, 30.0])
+        tri = (centre + rng.normal(size=(3, 3)) * rng.uniform(5, 120)).astype(np.float32)
+        margin = box_tri_margin(tri.astype(np.float64))
+        if abs(margin) < 0.05:
+            continue                      # too close to touching to call in float32
+        lib().oracle_probe_box_tri_sat((F * 9)(*tri.reshape(-1)), C.byref(ov), C.byref(ax), C.byref(dp), axis)
+        checked += 1
+        assert bool(ov.value) == (margin > 0), (tri, margin)
+        if ov.value:
+            hits += 1
+            a = np.array(list(axis), np.float64)
+            assert 0 <= ax.value < 13 and dp.value >= 0 and abs(np.linalg.norm(a) - 1) < 1e-5
+            moved = [box_tri_margin(tri + s * (dp.value + 0.05) * a) for s in (1.0, -1.0)]
+            assert min(moved) < 0, (tri, dp.value, a, moved)
+    assert checked > 400 and hits > 50
+
+
+def test_box_box_sat_agrees_with_linear_programming():
+    rng = np.random.default_rng(6)
+    ov, ax, dp = C.c_int(), C.c_int(), F()
+    checked = hits = 0
+    for _ in range(400):
+        qa, qb = rng.normal(size=4), rng.normal(size=4)
+        qa /= np.linalg.norm(qa)
+        qb /= np.linalg.norm(qb)
+        ca = rng.uniform(-1000, 1000, 3)
+        cb = ca + rng.normal(size=3) * 80.0
+        qa32, qb32 = qa.astype(np.float32), qb.astype(np.float32)
+        ca32, cb32 = ca.astype(np.float32), cb.astype(np.float32)
+        margin = box_box_margin(ca32.astype(np.float64), qa32.astype(np.float64) / np.linalg.norm(qa32),
+                                cb32.astype(np.float64), qb32.astype(np.float64) / np.linalg.norm(qb32))
+        if abs(margin) < 0.05:
+            continue
+        lib().oracle_probe_box_box_sat((F * 3)(*ca32), (F * 4)(*qa32), (F * 3)(*cb32), (F * 4)(*qb32), C.byref(ov),
+                                       C.byref(ax), C.byref(dp))
+        checked += 1
+        assert bool(ov.value) == (margin > 0), (ca, qa, cb, qb, margin)
+        hits += ov.value
+        if ov.value:
+            assert 0 <= ax.value < 15 and dp.value >= 0
+    assert checked > 300 and hits > 50
+
+
+# ---------------------------------------------------------------- suspension rays by brute force
+
+ANCHORS = np.array([[37.3743, 25.9, 0.0], [37.3743, -25.9, 0.0], [-47.6257, 29.5, 0.0], [-47.6257, -29.5, 0.0]])
+RAY_LEN = np.array([26.755 + 12 + 12.5 - 2.5] * 2 + [25.055 + 12 + 15 - 2.5] * 2)
+HITBOX_OFFSET = np.array([13.87566, 0.0, 20.755])
+
+
+def _nearest_hit(start, d, tv):
+    """Nearest ray-triangle hit over the whole mesh in float64 (ray-plane
+    intersection, then an inside test by barycentric signs)."""
+    a, b, c = tv[:, 0], tv[:, 1], tv[:, 2]
+    n = np.cross(b - a, c - a)
+    den = n @ d
+    ok = np.abs(den) > 1e-9
+    t = np.where(ok, ((a - start) * n).sum(1) / np.where(ok, den, 1.0), np.inf)
+    p = start + t[:, None] * d
+    inside = ((np.cross(b - a, p - a) * n).sum(1) >= 0) & ((np.cross(c - b, p - b) * n).sum(1) >= 0) & \
+             ((np.cross(a - c, p - c) * n).sum(1) >= 0)
+    t = np.where(ok & inside & (t > 0), t, np.inf)
+    i = int(np.argmin(t))
+    return t[i], n[i] / np.linalg.norm(n[i])
+
+
+def test_suspension_rays_match_brute_force_over_the_mesh(arena):
+    """Each wheel's hit distance and normal equal the nearest hit over all
+    triangles (the cell run holds every triangle a ray can reach), for cars
+    over the floor, ramps and walls."""
+    verts, tris, _, _, _ = arena
+    tv = verts[tris].astype(np.float64)
+    rng = np.random.default_rng(9)
+    n = 128
+    env = OracleEnv(n, 1, 0, 0)
+    pos = np.stack([rng.uniform(-4000, 4000, n), rng.uniform(-5000, 5000, n), rng.uniform(5, 45, n)], 1)
+    tilt = rng.normal(size=(n, 3)) * 0.3
+    ang = np.linalg.norm(tilt, axis=1, keepdims=True)
+    q = np.concatenate([tilt / ang * np.sin(ang / 2), np.cos(ang / 2)], 1)
+    env.set_car(pos[:, None].astype(np.float32), q[:, None].astype(np.float32), np.zeros((n, 1, 3), np.float32),
+                np.zeros((n, 1, 3), np.float32), np.zeros((n, 1), np.bool_))
+    car, _, _ = env.export_state()
+    dist, normal, source = env.raycast()
+    hits = 0
+    for i in range(n):
+        cen = f32(car[CAR["CARL_CAR_CEN_0"]:CAR["CARL_CAR_CEN_0"] + 3, i])
+        qq = f32(car[CAR["CARL_CAR_ROT_0"]:CAR["CARL_CAR_ROT_0"] + 4, i])
+        R = _rot(qq / np.linalg.norm(qq))
+        d = -R[:, 2]
+        for k in range(4):
+            t, nrm = _nearest_hit(cen + R @ ANCHORS[k], d, tv)
+            if t <= RAY_LEN[k] + 1.0 - 1e-3:
+                hits += 1
+                assert source[i, k] == 1, (i, k, t)
+                assert abs(dist[i, k] - t) < 2e-3, (i, k, dist[i, k], t)
+                nrm = -nrm if nrm @ d > 0 else nrm
+                assert np.abs(normal[i, k] - nrm).max() < 1e-5
+            elif t > RAY_LEN[k] + 1.0 + 1e-3:
+                assert source[i, k] == 0, (i, k, t)
+    assert hits > 150
+    env.close()

@@ -235,3 +235,106 @@ def test_boost_pad_table_matches_module_constants():
     pads = GOLDEN["boost_pads"]
     assert [list(p) for p in carl_amd.BOOST_PAD_POSITIONS] == [p[:3] for p in pads]
     assert [p[3] for p in pads] == [1] * 6 + [0] * 28  # big pads first
+
+
+# ---------------------------------------------------------------- tests/test_resets.py behaviours
+
+def reset_values(n, n_cars):
+    """The reset inputs of tests/test_resets.py:28-72 (ball at z 800 moving +x,
+    cars in a row at y -1000, last car demoed, boost 61, held-jump internals)."""
+    ball_pos = np.zeros((n, 3), np.float32)
+    ball_pos[:, 2] = 800
+    ball_vel = np.zeros((n, 3), np.float32)
+    ball_vel[:, 0] = 170
+    car_pos = np.zeros((n, n_cars, 3), np.float32)
+    car_pos[..., 0] = np.arange(n_cars) * 250 - 500
+    car_pos[..., 1] = -1000
+    car_pos[..., 2] = 17
+    rot = np.zeros((n, n_cars, 4), np.float32)
+    rot[..., 3] = 1
+    demoed = np.zeros((n, n_cars), np.bool_)
+    demoed[:, -1] = True
+    internal = np.zeros((n, n_cars, 19), np.float32)
+    internal[..., 3] = 1
+    internal[..., 5] = 1
+    return dict(ball_position=ball_pos, ball_velocity=ball_vel, ball_angular_velocity=np.zeros((n, 3), np.float32),
+                car_position=car_pos, car_rotation=rot, car_velocity=np.zeros((n, n_cars, 3), np.float32),
+                car_angular_velocity=np.zeros((n, n_cars, 3), np.float32), car_demoed=demoed,
+                car_boost=np.full((n, n_cars), 61, np.float32), car_internal_state=internal,
+                blue_score=np.full(n, 2, np.int32), orange_score=np.full(n, 1, np.int32),
+                episode_ticks=np.full(n, 23, np.int32))
+
+
+def test_restored_match_clock_enters_overtime_or_truncates():
+    """tests/test_resets.py:351-381: max_ticks 4, overtime 2; a tied restored
+    match enters overtime, the other truncates; overtime then expires."""
+    env = OracleEnv(2, 1, 1, 7)
+    env.set_param(0, 4)   # max_ticks
+    env.set_param(1, 2)   # overtime_timeout_ticks
+    v = reset_values(2, 2)
+    v["orange_score"][0] = 2
+    v["episode_ticks"][:] = 3
+    env.apply_reset_state(**v)
+    zero = np.zeros((2, 2, 7), np.float32)
+    env.step(zero)
+    assert env.get("dones").tolist() == [False, True]
+    assert env.get("overtime").tolist() == [True, False]
+    assert env.get("transition_episode_ticks").tolist() == [4, 4]
+    for _ in range(2):
+        env.step(zero)
+    assert env.get("dones").tolist() == [True, False]
+    assert bool(env.get("transition_overtime")[0])
+    assert not env.get("overtime").any()
+    env.close()
+
+
+@pytest.mark.parametrize("masked", [False, True])
+def test_restored_contacts_use_the_complete_scene(masked):
+    """tests/test_resets.py:289-323: the top car's wheels rest on the bottom
+    car (z 257 over z 200, both above the floor's reach): grounded only on top;
+    a demoed restored car is never grounded."""
+    env = OracleEnv(1, 1, 1, 7, previous_controls=True)
+    v = reset_values(1, 2)
+    v["car_position"][0] = [[0, 0, 257], [0, 0, 200]]
+    v["car_demoed"][:] = False
+    mask = np.ones(1, np.bool_) if masked else None
+    env.apply_reset_state(**v, reset_mask=mask)
+    state = env.get("state")
+    cars = state[:, 9:9 + 2 * 22].reshape(1, 2, 22)
+    np.testing.assert_array_equal(cars[..., :3], v["car_position"])
+    np.testing.assert_array_equal(cars[..., 3:6], v["car_velocity"])
+    assert cars[0, 0, 16] == 1.0 and cars[0, 1, 16] == 0.0   # OBS_ON_GROUND
+    assert not cars[..., 21].any()                           # STATE_BALL_TOUCH
+    v["car_demoed"][:, 0] = True
+    env.apply_reset_state(**v, reset_mask=mask)
+    assert env.get("obs")[0, 0, 9 + 16] == 0.0
+    env.close()
+
+
+def test_observation_layout_closed_form():
+    """include/Physics/Observations.cuh:97-238 layout for a set state: ball
+    block, ego car first, others after, orange cars seeing the field point
+    mirrored (x, y negated), boost pads, all at the offsets of DLPack.h."""
+    env = OracleEnv(1, 1, 1, 7)
+    ball_p, ball_v, ball_w = [100.0, -200.0, 300.0], [10.0, 20.0, -30.0], [0.5, -0.25, 1.0]
+    env.set_ball(np.array([ball_p], np.float32), np.array([ball_v], np.float32), np.array([ball_w], np.float32))
+    cp = np.array([[[-500.0, 1000.0, 17.0], [700.0, -1500.0, 17.0]]], np.float32)
+    cv = np.array([[[100.0, 0.0, 0.0], [0.0, -200.0, 0.0]]], np.float32)
+    rot = np.zeros((1, 2, 4), np.float32)
+    rot[..., 3] = 1
+    env.set_car(cp, rot, cv, np.zeros((1, 2, 3), np.float32), np.zeros((1, 2), np.bool_),
+                boost=np.array([[40.0, 70.0]], np.float32))
+    obs = env.get("obs")[0]
+    blue, orange = obs[0], obs[1]
+    np.testing.assert_array_equal(blue[0:3], ball_p)
+    np.testing.assert_array_equal(blue[3:6], ball_v)
+    np.testing.assert_array_equal(blue[6:9], ball_w)
+    np.testing.assert_array_equal(blue[9:12], cp[0, 0])           # ego = own car
+    np.testing.assert_array_equal(blue[9 + 21:9 + 24], cp[0, 1])   # then the other car
+    assert blue[9 + 15] == 40.0 and blue[9 + 21 + 15] == 70.0     # OBS_BOOST
+    mirror = np.array([-1.0, -1.0, 1.0], np.float32)
+    np.testing.assert_array_equal(orange[0:3], np.array(ball_p, np.float32) * mirror)
+    np.testing.assert_array_equal(orange[3:6], np.array(ball_v, np.float32) * mirror)
+    np.testing.assert_array_equal(orange[9:12], cp[0, 1] * mirror)  # orange ego first, mirrored
+    np.testing.assert_array_equal(orange[9 + 21:9 + 24], cp[0, 0] * mirror)
+    env.close()
