@@ -30,8 +30,9 @@
  *   carl_env_synchronize   <- cudaStreamSynchronize calls python/carl.cu:419,505,663
  *   carl_exclusive_scan_i32 <- PrefixSum::scanOnStream   src/RLEnvironment.cu:18-38
  *
- * carl_env_enable_timing / carl_env_tick_timing have no reference counterpart:
- * they time the tick kernel with HIP events on the environment stream.
+ * carl_env_enable_timing / carl_env_tick_timing / carl_tick_kernel_name have no
+ * reference counterpart: they time the tick kernels with HIP events on the
+ * environment stream.
  * carl_env_export_state / carl_env_import_state have no reference counterpart;
  * they expose the persistent per-car / per-simulation state (layout below) so
  * that a CPU model can be stepped from the same state and compared field by

@@ -19,6 +19,13 @@
  *     of an equal zero, which the comparison form pins).
  * The HIP engine follows the same contract, which is what lets a simulation
  * tick agree bit for bit between the two.
+ *
+ * Pinned by the reference's own known-answer tests, its tables, closed forms,
+ * linear-programming SAT checks and brute-force mesh searches (tests/).
+ * PARITY UNPINNED (no independent check; engine and oracle agree with each
+ * other only): suspension forces beyond the at-rest equilibrium, the PGS
+ * solver internals, car-car bump/demo impulses, the car-ball extra impulse,
+ * the ball contact reduction and edge adjustment.
  */
 #ifndef CARL_ORACLE_MATH_H
 #define CARL_ORACLE_MATH_H
