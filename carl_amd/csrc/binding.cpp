@@ -106,6 +106,16 @@ struct TensorView {
     const void* data() const { return static_cast<const char*>(tensor.data) + tensor.byte_offset; }
 };
 
+// An empty simulation_indices tensor may have a null data pointer; the C-ABI
+// reads a null index pointer as "every simulation", so an empty selection
+// passes a dummy (never dereferenced) pointer instead.
+const int64_t kNoIndex = 0;
+const int64_t* selectionPointer(const TensorView& sel)
+{
+    const auto* p = static_cast<const int64_t*>(sel.data());
+    return p ? p : &kNoIndex;
+}
+
 struct PendingInput {
     std::vector<py::object> inputs;
     hipEvent_t done = nullptr;
@@ -279,7 +289,7 @@ public:
         const int64_t* idx = nullptr;
         if (!indices.is_none()) {
             sel.emplace(selection(indices));
-            idx = static_cast<const int64_t*>(sel->data());
+            idx = selectionPointer(*sel);
             n = (int)sel->tensor.shape[0];
         }
         const auto p = view(position, "position", { n, 3 }, kDLFloat, 32);
@@ -297,7 +307,7 @@ public:
         const int64_t* idx = nullptr;
         if (!indices.is_none()) {
             sel.emplace(selection(indices));
-            idx = static_cast<const int64_t*>(sel->data());
+            idx = selectionPointer(*sel);
             n = (int)sel->tensor.shape[0];
         }
         const auto p = view(position, "position", { n, nCars_, 3 }, kDLFloat, 32);
@@ -327,7 +337,7 @@ public:
         const int64_t* idx = nullptr;
         if (!indices.is_none()) {
             sel.emplace(selection(indices));
-            idx = static_cast<const int64_t*>(sel->data());
+            idx = selectionPointer(*sel);
             n = (int)sel->tensor.shape[0];
         }
         if (!mask.is_none()) maskView.emplace(view(mask, "reset_mask", { nSim_ }, kDLBool, 8));
@@ -388,7 +398,7 @@ public:
         const int64_t* idx = nullptr;
         if (!indices.is_none()) {
             sel.emplace(selection(indices));
-            idx = static_cast<const int64_t*>(sel->data());
+            idx = selectionPointer(*sel);
             n = (int)sel->tensor.shape[0];
         }
         const auto b = view(blue, "blue_score", { n }, kDLInt, 32);
@@ -405,7 +415,7 @@ public:
         const int64_t* idx = nullptr;
         if (!indices.is_none()) {
             sel.emplace(selection(indices));
-            idx = static_cast<const int64_t*>(sel->data());
+            idx = selectionPointer(*sel);
             n = (int)sel->tensor.shape[0];
         }
         check(carl_env_reset_pads(env_, idx, n));
