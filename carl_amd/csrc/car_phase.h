@@ -949,6 +949,9 @@ struct ContactLds {
     int satHits[64];
     unsigned long long rayKey[kWheels][64];
     unsigned long long bestKey[64];
+    // SAT hits awaiting contact generation, in run order: owner << 24 | item
+    int hitQ[128];
+    int hitN;
 };
 
 constexpr unsigned long long kNoKey = ~0ull;
@@ -995,17 +998,51 @@ DI void contactItem(const Dev& d, ContactLds& L, const Tri& t, int o, int q, int
     if (!hit) return;
     // hits of this owner earlier in the run: previous rounds + lower lanes now
     const int firstLane = L.excl[o] - base > 0 ? L.excl[o] - base : 0;
-    const unsigned long long below = (lane ? (~0ull >> (64 - lane)) : 0ull) & (~0ull << firstLane);
-    const int rank = L.satHits[o] + __popcll(mask & below);
-    if (rank < kMaxTriHits) {
+    const unsigned long long lower = lane ? (~0ull >> (64 - lane)) : 0ull;
+    const int rank = L.satHits[o] + __popcll(mask & lower & (~0ull << firstLane));
+    // hits that take part are queued; their contacts are generated together
+    // (contactFlush), so the expensive clipping runs on dense lanes
+    const bool keep = rank < kMaxTriHits;
+    const unsigned long long kept = __ballot(keep);
+    const int n = L.hitN;
+    if (keep) L.hitQ[n + __popcll(kept & lower)] = (o << 24) | q;
+    atomicAdd(&L.satHits[o], 1);
+    if (lane == (int)__builtin_ctzll(mask)) L.hitN = n + __popcll(kept);
+}
+
+// Contact generation for the first min(hitN, 64) queued hits (all lanes of
+// the wave call it); the rest move to the front of the queue.
+DI void contactFlush(const Dev& d, ContactLds& L, int lane, bool all)
+{
+    const int n = L.hitN;
+    if (n < 64 && !(all && n > 0)) return;
+    const int take = n < 64 ? n : 64;
+    if (lane < take) {
+        const int e = L.hitQ[lane];
+        const int o = e >> 24, q = e & 0xffffff;
+        const Tri t = loadTri(d.arena, L.first[o] + q);
+        const V3 cen{ L.cen[0][o], L.cen[1][o], L.cen[2][o] };
+        const Q4 rot{ L.rot[0][o], L.rot[1][o], L.rot[2][o], L.rot[3][o] };
+        const LocalTri lt = toLocal(t, cen, rot);
+        const Sat sat = boxTriSat(lt);
         V3 near[kMaxManifold];
 #pragma unroll
         for (int i = 0; i < kMaxManifold; i++) near[i] = V3{ L.nearPos[i][0][o], L.nearPos[i][1][o], L.nearPos[i][2][o] };
         Contact c;
         float value = kFltMax;
-        if (triBestContact(lt, sat, near, L.nearN[o], c, value)) atomicMin(&L.bestKey[o], contactKey(value, q));
+        if (sat.overlap && triBestContact(lt, sat, near, L.nearN[o], c, value))
+            atomicMin(&L.bestKey[o], contactKey(value, q));
     }
-    atomicAdd(&L.satHits[o], 1);
+    const int rest = n - take;
+    const int moved = lane < rest ? L.hitQ[take + lane] : 0;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane < rest) L.hitQ[lane] = moved;
+    if (lane == 0) L.hitN = rest;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 // Owner side, before the search: pose, rays and (with sat) the plane points
@@ -1035,6 +1072,7 @@ DI void contactPrepare(ContactLds& L, int lane, bool sat, V3 cen, Q4 rot, int fi
     }
     L.satHits[lane] = 0;
     L.bestKey[lane] = kNoKey;
+    if (lane == 0) L.hitN = 0;
 }
 
 // Owner side, after the search: wheel hits (arena winner, then cars and the

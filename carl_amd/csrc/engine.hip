@@ -90,7 +90,11 @@ __global__ __launch_bounds__(kContactBlock) void contactKernel(Dev d, uint32_t* 
     __syncthreads();
     waveItemsPipelined(
         bp.count, L.excl, [&](int o, int q, bool valid) { return contactFetch(d, L, o, q, valid); },
-        [&](const Tri& t, int o, int q, int base) { contactItem(d, L, t, o, q, base, lane); });
+        [&](const Tri& t, int o, int q, int base) { contactItem(d, L, t, o, q, base, lane); },
+        [&](bool last) {
+            contactFlush(d, L, lane, false);
+            if (last) contactFlush(d, L, lane, true);
+        });
     __syncthreads();
     if (!ok) return;
     Wheels w;

@@ -57,9 +57,11 @@ __device__ __forceinline__ void waveItems(int count, int* excl, Body&& body)
 // waveItems with a two-stage pipeline: fetch(owner, item) issues the loads of
 // the next round before process(value, owner, item, base) runs on the current
 // one, so each round's memory latency overlaps the previous round's work.
-// Same visiting order and lane placement as waveItems.
-template <typename Fetch, typename Process>
-__device__ __forceinline__ void waveItemsPipelined(int count, int* excl, Fetch&& fetch, Process&& process)
+// Same visiting order and lane placement as waveItems.  after(last) runs on
+// every lane of the wave once per round, after process.
+template <typename Fetch, typename Process, typename After>
+__device__ __forceinline__ void waveItemsPipelined(int count, int* excl, Fetch&& fetch, Process&& process,
+                                                   After&& after)
 {
     const int lane = (int)(threadIdx.x & 63);
     const int incl = waveInclusiveScan(count);
@@ -91,10 +93,18 @@ __device__ __forceinline__ void waveItemsPipelined(int count, int* excl, Fetch&&
         }
         auto next = fetch(on, qn, jn < total);
         if (base + lane < total) process(cur, o, q, base);
+        after(base + 64 >= total);   // every lane; true after the last round
         cur = next;
         o = on;
         q = qn;
     }
+}
+
+// Without a per-round hook.
+template <typename Fetch, typename Process>
+__device__ __forceinline__ void waveItemsPipelined(int count, int* excl, Fetch&& fetch, Process&& process)
+{
+    waveItemsPipelined(count, excl, fetch, process, [](bool) {});
 }
 
 }  // namespace carl
