@@ -212,8 +212,66 @@ std::string buildArena(const std::string& objPath, HostArena& out)
                                 e2.z, b.x, b.y, b.z, c.x, c.y, c.z, tag };
         std::memcpy(&out.triRecords[16 * (size_t)t], rec, sizeof rec);
     }
-    for (int r = 0; r < nRefs; r++)
-        std::memcpy(&out.records[16 * (size_t)r], &out.triRecords[16 * (size_t)out.cellTris[r]], 16 * sizeof(float));
+    // Screening data of the contact search, per triangle (16 floats):
+    //   box min xyz, n.x | box max xyz, n.y | n.z, n.v0, rayCond, rayTol |
+    //   satS1, satS2, satS3, eps * longest edge
+    // n is the unit normal of the plane through v0 along e1, e2 (the edges the
+    // ray test uses).  The bounds come from the rounding analysis of the float
+    // tests the screen stands in for (float32, no contraction, eps = 2^-24,
+    // g = 16 eps, ray starts within T = 32768 of v0, rays at most 64 long,
+    // s = |e1 x e2| / (|e1| |e2|)); each is enlarged by a quarter:
+    //   rayTol   an accepted ray hit lies within (g (64 + T) + 2^-16) / s of
+    //            the plane;
+    //   rayCond  it lies within rayCond / |n.dir| of a point of the triangle,
+    //            rayCond = g (3 T + |e1| + |e2| + 64) / s;
+    //   satS*    the SAT normal axis, computed from vertices rotated with
+    //            error at most 96 eps D (D the distance to the box centre),
+    //            deviates from n by at most
+    //            dn = d S1 + d^2 S2 + S3, d = 192 eps D + eps * longest edge,
+    //            with a = |v1 - v0|, b = |v2 - v1|, 2A = |(v1 - v0) x (v2 - v1)|:
+    //            S1 = 2 (a + b) / 2A, S2 = 2 / 2A, S3 = 12 eps a b / 2A + 4 eps.
+    // A mesh with vertices beyond 8192 (the ray bound T no longer holds) gets
+    // bounds that screen nothing.
+    float vmaxAbs = 0.f;
+    for (const V3& v : verts) vmaxAbs = std::max(vmaxAbs, std::max(std::fabs(v.x), std::max(std::fabs(v.y), std::fabs(v.z))));
+    std::vector<float> screen(16 * (size_t)nTris);
+    const double eps = std::ldexp(1.0, -24), g = 16.0 * eps, T = 32768.0, L = 64.0, grow = 1.25;
+    for (int t = 0; t < nTris; t++) {
+        const float* rec = &out.triRecords[16 * (size_t)t];
+        const double ax = rec[0], ay = rec[1], az = rec[2];
+        const double e1x = rec[3], e1y = rec[4], e1z = rec[5], e2x = rec[6], e2y = rec[7], e2z = rec[8];
+        const double nx = e1y * e2z - e1z * e2y, ny = e1z * e2x - e1x * e2z, nz = e1x * e2y - e1y * e2x;
+        const double nl = std::sqrt(nx * nx + ny * ny + nz * nz);
+        const double l1 = std::sqrt(e1x * e1x + e1y * e1y + e1z * e1z);
+        const double l2 = std::sqrt(e2x * e2x + e2y * e2y + e2z * e2z);
+        const double sinA = nl / (l1 * l2);
+        double rayTol = (g * (L + T) + std::ldexp(1.0, -16)) / sinA * grow + 0.05;
+        double rayCond = g * (3.0 * T + l1 + l2 + L) / sinA * grow + 1e-3;
+        // SAT edges from the vertices themselves
+        const double p0x = rec[0], p0y = rec[1], p0z = rec[2], p1x = rec[9], p1y = rec[10], p1z = rec[11];
+        const double p2x = rec[12], p2y = rec[13], p2z = rec[14];
+        const double fx = p1x - p0x, fy = p1y - p0y, fz = p1z - p0z, hx = p2x - p1x, hy = p2y - p1y, hz = p2z - p1z;
+        const double kx = p0x - p2x, ky = p0y - p2y, kz = p0z - p2z;
+        const double sa = std::sqrt(fx * fx + fy * fy + fz * fz), sb = std::sqrt(hx * hx + hy * hy + hz * hz);
+        const double sc = std::sqrt(kx * kx + ky * ky + kz * kz);
+        const double cx = fy * hz - fz * hy, cy = fz * hx - fx * hz, cz = fx * hy - fy * hx;
+        const double a2 = std::sqrt(cx * cx + cy * cy + cz * cz);
+        double s1 = 2.0 * (sa + sb) / a2 * grow, s2 = 2.0 / a2 * grow, s3 = (12.0 * eps * sa * sb / a2 + 4.0 * eps) * grow;
+        const double epsEdge = eps * std::max(sa, std::max(sb, sc)) * grow;
+        if (!(vmaxAbs < 8192.f) || !(sinA > 1e-9) || !(rayTol < 1e30) || !(rayCond < 1e30)) rayTol = rayCond = 3e38;
+        if (!(vmaxAbs < 8192.f) || !(a2 > 1e-9) || !(s1 < 1e30) || !(s2 < 1e30)) s1 = s2 = s3 = 3e38;
+        const float f[16] = { lo[t].x, lo[t].y, lo[t].z, (float)(nx / nl),
+                              hi[t].x, hi[t].y, hi[t].z, (float)(ny / nl),
+                              (float)(nz / nl), (float)((nx * ax + ny * ay + nz * az) / nl), (float)rayCond, (float)rayTol,
+                              (float)s1, (float)s2, (float)s3, (float)epsEdge };
+        std::memcpy(&screen[16 * (size_t)t], f, sizeof f);
+    }
+    out.refBoxes.assign(16 * (size_t)nRefs, 0.f);
+    for (int r = 0; r < nRefs; r++) {
+        const int t = out.cellTris[r];
+        std::memcpy(&out.records[16 * (size_t)r], &out.triRecords[16 * (size_t)t], 16 * sizeof(float));
+        std::memcpy(&out.refBoxes[16 * (size_t)r], &screen[16 * (size_t)t], 16 * sizeof(float));
+    }
     return "";
 }
 

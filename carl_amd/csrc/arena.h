@@ -15,6 +15,7 @@ struct HostArena {
     std::vector<int> cellTris;      // triangle per cell reference, ascending within a cell
     std::vector<float> records;     // 16 floats per cell reference (device layout, see state.h)
     std::vector<float> triRecords;  // the same 16 floats per triangle, by triangle index
+    std::vector<float> refBoxes;    // 16 floats per cell reference: contact-search screening data
 };
 
 // Parse, weld and index the mesh.  Returns "" on success, else the error text.

@@ -624,6 +624,8 @@ PYBIND11_MODULE(_carl, m)
                       [](Env& e, int v) { e.setParam(CARL_PARAM_FRAMESKIP, v); })
         .def_property("tick_streams", [](Env& e) { return e.param(CARL_PARAM_TICK_STREAMS); },
                       [](Env& e, int v) { e.setParam(CARL_PARAM_TICK_STREAMS, v); })
+        .def_property("contact_screen", [](Env& e) { return e.param(CARL_PARAM_CONTACT_SCREEN); },
+                      [](Env& e, int v) { e.setParam(CARL_PARAM_CONTACT_SCREEN, v); })
         .def_property_readonly("obs_dim", [](Env& e) { return e.param(CARL_PARAM_OBS_DIM); })
         .def_property_readonly("act_dim", [](Env& e) { return e.param(CARL_PARAM_ACT_DIM); })
         .def_property_readonly("action_nvec", &Env::actionNvec)

@@ -930,137 +930,266 @@ DI int buildManifold(const Dev& d, V3 cen, Q4 rot, int bestRef, ManPt* pts)
 
 // ------------------------------------------------ cooperative cell search
 //
-// One wave searches the cell runs of its 64 cars together (waveItems): each
-// (car, cell triangle) pair runs the four suspension rays and the car-arena
-// SAT.  Per wheel the nearest ray hit is kept by an LDS atomic minimum of
-// (distance, position in the cell run), which is the sequential result: the
-// reference walks the run in order and keeps strictly nearer hits.  SAT hits
-// are ranked in run order (only the first kMaxTriHits take part, as in the
-// sequential walk) and their contacts compete by contactKey, whose minimum is
-// the first deepest contact of the walk.
+// One wave searches the cell runs of its cars together, in three stages that
+// each keep all 64 lanes busy:
+//   screen every (car, cell triangle) item against bounds that prove the
+//          float tests of the next stage reject it; the others are queued in
+//          run order;
+//   heavy  queued items, 64 at a time: the four suspension rays and the
+//          box-triangle SAT; SAT hits are ranked in run order and the first
+//          kMaxTriHits of each car are queued;
+//   clip   queued hits, 64 at a time: contact generation.
+// Per wheel the nearest ray hit is kept by an LDS atomic minimum of
+// (distance, position in the run): the sequential walk keeps strictly nearer
+// hits, so this is its result.  Contacts compete by contactKey, whose minimum
+// is the first deepest contact of the walk.
+//
+// Screening is exact, not approximate: an item is dropped only when bounds
+// from the rounding analysis of the heavy stage's float tests (arena.cpp)
+// prove that both reject it:
+//   SAT    the car takes no part in the car-arena search, or the triangle's
+//          box, projected on one of the car's box axes, lies more than
+//          kSatMargin beyond the box face (the float SAT tests those axes on
+//          rotated vertices whose rounding stays below 0.25 within the
+//          screening range), or the car box lies beyond the triangle's plane
+//          by more than the deviation bound of the float normal axis allows;
+//   rays   the segments of all four rays keep a distance beyond the
+//          triangle's plane tolerance from its plane, or the triangle's box
+//          lies a gap G beyond their box with |n.dir| (G - kGapSlack) above
+//          its conditioning bound: an accepted hit lies within those bounds
+//          of the plane and of the triangle.
+// Cars outside the screening range (|position| >= kScreenRange on an axis, or
+// a degenerate quaternion) are not screened.
+constexpr float kSatMargin = 0.5f;
+constexpr float kGapSlack = 0.05f;
+constexpr float kPlaneSlack = 0.05f;
+constexpr float kScreenRange = 8192.f;
+constexpr float kRotErr = 100.f * 0x1p-24f;    // rotated vertex error per unit of distance (96 eps, rounded up)
+constexpr float kRotErr2 = 2.f * kRotErr;      // the same for an edge (two vertices)
+constexpr float kHalfLen = 80.f;               // |kHalf| rounded up
+
 struct ContactLds {
     int excl[64];
     int first[64];   // first cell reference of the owner's run
     int satOn[64];   // owner takes part in the car-arena search (not demoed)
-    float cen[3][64], rot[4][64], dir[3][64];
+    float rot[4][64];
     float start[kWheels][3][64];
+    // screening, per owner: (cen, rayLo.x) (ax, rayLo.y) (ay, rayLo.z)
+    // (az, rayHi.x) (rayHi.y, rayHi.z, screened, satOn); ax..az are the car's
+    // box axes, ray* the box of the four ray segments
+    float4 scr[5][64];
     float nearPos[kMaxManifold][3][64];
     int nearN[64];
     int satHits[64];
     unsigned long long rayKey[kWheels][64];
     unsigned long long bestKey[64];
-    // SAT hits awaiting contact generation, in run order: owner << 24 | item
-    int hitQ[128];
-    int hitN;
+    float rayNrm[kWheels][3][64];   // surface normal of each wheel's nearest arena hit
+    // screened items in run order, entries owner << 24 | item
+    int candQ[128];
+    int candN;
 };
 
 constexpr unsigned long long kNoKey = ~0ull;
 
-// the cell triangle of item q of owner o (a dummy load of reference 0 for
-// lanes without an item keeps the pipeline uniform)
-DI Tri contactFetch(const Dev& d, const ContactLds& L, int o, int q, bool valid)
+DI V3 ownerCen(const ContactLds& L, int o)
 {
-    return loadTri(d.arena, valid ? L.first[o] + q : 0);
+    const float4 c = L.scr[0][o];
+    return V3{ c.x, c.y, c.z };
+}
+// suspension ray direction: minus the car's up axis
+DI V3 ownerDir(const ContactLds& L, int o)
+{
+    const float4 a = L.scr[3][o];
+    return V3{ -a.x, -a.y, -a.z };
 }
 
-DI void contactItem(const Dev& d, ContactLds& L, const Tri& t, int o, int q, int base, int lane)
+struct RefBox {
+    float4 lo, hi, pl, sat;
+};
+
+// screening data of item q of owner o (reference 0 for lanes without an item)
+DI RefBox contactFetch(const Dev& d, const ContactLds& L, int o, int q, bool valid)
 {
-    const V3 dir{ L.dir[0][o], L.dir[1][o], L.dir[2][o] };
-    const V3 pv = cross(dir, t.e2);
-    const float det = dot(t.e1, pv);
-    if (!(fabsf(det) < 1e-8f)) {
-        const float invDet = 1.f / det;
+    const int ref = valid ? L.first[o] + q : 0;
+    const float4* b = d.arena.box + 4 * (size_t)ref;
+    return RefBox{ b[0], b[1], b[2], b[3] };
+}
+
+DI void waveSync()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+DI unsigned long long lanesBelow(int lane) { return lane ? (~0ull >> (64 - lane)) : 0ull; }
+
+DI bool boxAxisMiss(V3 axis, V3 w, V3 half, float face)
+{
+    return fabsf(dot(axis, w)) - dot(vabs(axis), half) > face + kSatMargin;
+}
+
+// screen stage: queue the item unless the heavy stage provably rejects it
+DI void contactScreen(ContactLds& L, const RefBox& b, int o, int q, int lane)
+{
+    const float4 s0 = L.scr[0][o], s1 = L.scr[1][o], s2 = L.scr[2][o], s3 = L.scr[3][o], s4 = L.scr[4][o];
+    const V3 tlo{ b.lo.x, b.lo.y, b.lo.z }, thi{ b.hi.x, b.hi.y, b.hi.z };
+    const V3 rlo{ s0.w, s1.w, s2.w }, rhi{ s3.w, s4.x, s4.y };
+    const V3 az{ s3.x, s3.y, s3.z };
+    const V3 w = (tlo + thi) * 0.5f - V3{ s0.x, s0.y, s0.z };
+    const V3 half = (thi - tlo) * 0.5f;
+    const V3 ax{ s1.x, s1.y, s1.z }, ay{ s2.x, s2.y, s2.z };
+    const V3 n{ b.lo.w, b.hi.w, b.pl.x };
+    // the car box against the triangle's plane, within the normal axis bound
+    const float dist = l1norm(w) + l1norm(half);
+    const float dev = kRotErr2 * dist + b.sat.w;
+    const float dn = (dev * b.sat.x + dev * dev * b.sat.y) + b.sat.z;
+    const float boxR = dot(vabs(V3{ dot(n, ax), dot(n, ay), dot(n, az) }), kHalf);
+    const float planeGap = fabsf(b.pl.y - dot(n, V3{ s0.x, s0.y, s0.z })) - boxR;
+    const float planeTol = (dn * (dist + kHalfLen) + kRotErr * dist) + kPlaneSlack;
+    const bool satMiss = s4.w == 0.f || boxAxisMiss(ax, w, half, kHalf.x) || boxAxisMiss(ay, w, half, kHalf.y) ||
+                         boxAxisMiss(az, w, half, kHalf.z) || (dn <= 0.5f && planeGap > planeTol);
+    const float gap = fmax_(fmax_(fmax_(tlo.x - rhi.x, rlo.x - thi.x), fmax_(tlo.y - rhi.y, rlo.y - thi.y)),
+                            fmax_(tlo.z - rhi.z, rlo.z - thi.z));
+    const float cosDir = fabsf(dot(n, az)) - 1e-6f;
+    const float sc = dot(n, (rlo + rhi) * 0.5f) - b.pl.y;
+    const float sh = dot(vabs(n), (rhi - rlo) * 0.5f);
+    const bool rayMiss = (gap > kGapSlack && cosDir * (gap - kGapSlack) > b.pl.z) || sc - sh > b.pl.w ||
+                         sc + sh < -b.pl.w;
+    const bool keep = s4.z == 0.f || !(satMiss && rayMiss);
+    const unsigned long long m = __ballot(keep);
+    const int n0 = L.candN;
+    if (keep) L.candQ[n0 + __popcll(m & lanesBelow(lane))] = (o << 24) | q;
+    if (lane == (int)__builtin_ctzll(__ballot(1))) L.candN = n0 + __popcll(m);
+}
+
+// heavy stage for the first min(candN, 64) queued items; the rest move up.
+// Queue entries are in run order, so one owner's entries in a chunk sit on
+// consecutive lanes.  SAT hits within the owner's first kMaxTriHits generate
+// their contacts here; each wheel's nearest ray hit so far leaves its normal
+// in LDS, so the owner needs no triangle load afterwards.
+DI void contactHeavy(const Dev& d, ContactLds& L, int lane)
+{
+    const int n = L.candN;
+    const int take = n < 64 ? n : 64;
+    const bool active = lane < take;
+    const int e = active ? L.candQ[lane] : 0;
+    const int o = e >> 24, q = e & 0xffffff;
+    bool rayHit = false;
+    V3 fn = kZero;   // surface normal facing against the rays, for lanes with a ray hit
+    if (active) {
+        const Tri t = loadTri(d.arena, L.first[o] + q);
+        const V3 dir = ownerDir(L, o);
+        const V3 pv = cross(dir, t.e2);
+        const float det = dot(t.e1, pv);
+        if (!(fabsf(det) < 1e-8f)) {
+            const float invDet = 1.f / det;
 #pragma unroll
-        for (int k = 0; k < kWheels; k++) {
-            const V3 st{ L.start[k][0][o], L.start[k][1][o], L.start[k][2][o] };
-            const V3 tv = st - t.v0;
-            const float u = invDet * dot(tv, pv);
-            if (u < 0.f || u > 1.f) continue;
-            const V3 qv = cross(tv, t.e1);
-            const float v = invDet * dot(dir, qv);
-            if (v < 0.f || u + v > 1.f) continue;
-            const float hd = invDet * dot(t.e2, qv);
-            if (hd <= 0.f || hd >= wheelRay(k) + 1.f) continue;
-            atomicMin(&L.rayKey[k][o], ((unsigned long long)__float_as_uint(hd) << 32) | (uint32_t)q);
+            for (int k = 0; k < kWheels; k++) {
+                const V3 st{ L.start[k][0][o], L.start[k][1][o], L.start[k][2][o] };
+                const V3 tv = st - t.v0;
+                const float u = invDet * dot(tv, pv);
+                if (u < 0.f || u > 1.f) continue;
+                const V3 qv = cross(tv, t.e1);
+                const float v = invDet * dot(dir, qv);
+                if (v < 0.f || u + v > 1.f) continue;
+                const float hd = invDet * dot(t.e2, qv);
+                if (hd <= 0.f || hd >= wheelRay(k) + 1.f) continue;
+                rayHit = true;
+                atomicMin(&L.rayKey[k][o], ((unsigned long long)__float_as_uint(hd) << 32) | (uint32_t)q);
+            }
+        }
+        // arena triangles are non-degenerate (|e1 x e2|^2 > 1e-12 is checked
+        // when the mesh is built), so the first branch is the one taken
+        if (rayHit) {
+            fn = cross(t.e1, t.e2);
+            const float nl = lensq(fn);
+            if (nl > 1e-12f) {
+                fn = fn * rsqrt_(nl);
+                if (dot(fn, dir) > 0.f) fn = -fn;
+            } else {
+                fn = -dir;
+            }
+        }
+        bool hit = false;
+        LocalTri lt;
+        Sat sat;
+        if (L.satOn[o] && !t.plane) {
+            const Q4 rot{ L.rot[0][o], L.rot[1][o], L.rot[2][o], L.rot[3][o] };
+            lt = toLocal(t, ownerCen(L, o), rot);
+            sat = boxTriSat(lt);
+            hit = sat.overlap;
+        }
+        // rank among the owner's hits so far: earlier chunks + lower lanes of
+        // the owner's lane segment in this chunk
+        const int prevOwner = lane > 0 ? L.candQ[lane - 1] >> 24 : -1;
+        const unsigned long long starts = __ballot(o != prevOwner);
+        const unsigned long long upto = lane == 63 ? ~0ull : ((2ull << lane) - 1);
+        const int segStart = 63 - __clzll(starts & upto);
+        const unsigned long long hits = __ballot(hit);
+        const int rank = L.satHits[o] + __popcll(hits & lanesBelow(lane) & (~0ull << segStart));
+        if (hit) atomicAdd(&L.satHits[o], 1);
+        if (hit && rank < kMaxTriHits) {
+            V3 near[kMaxManifold];
+#pragma unroll
+            for (int i = 0; i < kMaxManifold; i++)
+                near[i] = V3{ L.nearPos[i][0][o], L.nearPos[i][1][o], L.nearPos[i][2][o] };
+            Contact c;
+            float value = kFltMax;
+            if (triBestContact(lt, sat, near, L.nearN[o], c, value)) atomicMin(&L.bestKey[o], contactKey(value, q));
         }
     }
-    bool hit = false;
-    LocalTri lt;
-    Sat sat;
-    if (L.satOn[o] && !t.plane) {
-        const V3 cen{ L.cen[0][o], L.cen[1][o], L.cen[2][o] };
-        const Q4 rot{ L.rot[0][o], L.rot[1][o], L.rot[2][o], L.rot[3][o] };
-        lt = toLocal(t, cen, rot);
-        sat = boxTriSat(lt);
-        hit = sat.overlap;
-    }
-    const unsigned long long mask = __ballot(hit);
-    if (!hit) return;
-    // hits of this owner earlier in the run: previous rounds + lower lanes now
-    const int firstLane = L.excl[o] - base > 0 ? L.excl[o] - base : 0;
-    const unsigned long long lower = lane ? (~0ull >> (64 - lane)) : 0ull;
-    const int rank = L.satHits[o] + __popcll(mask & lower & (~0ull << firstLane));
-    // hits that take part are queued; their contacts are generated together
-    // (contactFlush), so the expensive clipping runs on dense lanes
-    const bool keep = rank < kMaxTriHits;
-    const unsigned long long kept = __ballot(keep);
-    const int n = L.hitN;
-    if (keep) L.hitQ[n + __popcll(kept & lower)] = (o << 24) | q;
-    atomicAdd(&L.satHits[o], 1);
-    if (lane == (int)__builtin_ctzll(mask)) L.hitN = n + __popcll(kept);
-}
-
-// Contact generation for the first min(hitN, 64) queued hits (all lanes of
-// the wave call it); the rest move to the front of the queue.
-DI void contactFlush(const Dev& d, ContactLds& L, int lane, bool all)
-{
-    const int n = L.hitN;
-    if (n < 64 && !(all && n > 0)) return;
-    const int take = n < 64 ? n : 64;
-    if (lane < take) {
-        const int e = L.hitQ[lane];
-        const int o = e >> 24, q = e & 0xffffff;
-        const Tri t = loadTri(d.arena, L.first[o] + q);
-        const V3 cen{ L.cen[0][o], L.cen[1][o], L.cen[2][o] };
-        const Q4 rot{ L.rot[0][o], L.rot[1][o], L.rot[2][o], L.rot[3][o] };
-        const LocalTri lt = toLocal(t, cen, rot);
-        const Sat sat = boxTriSat(lt);
-        V3 near[kMaxManifold];
+    waveSync();
+    // the lane holding a wheel's current winner (its item is the key's low
+    // word, unique within the owner's run) records the winner's normal
+    if (rayHit) {
 #pragma unroll
-        for (int i = 0; i < kMaxManifold; i++) near[i] = V3{ L.nearPos[i][0][o], L.nearPos[i][1][o], L.nearPos[i][2][o] };
-        Contact c;
-        float value = kFltMax;
-        if (sat.overlap && triBestContact(lt, sat, near, L.nearN[o], c, value))
-            atomicMin(&L.bestKey[o], contactKey(value, q));
+        for (int k = 0; k < kWheels; k++) {
+            if ((uint32_t)L.rayKey[k][o] != (uint32_t)q) continue;
+            L.rayNrm[k][0][o] = fn.x; L.rayNrm[k][1][o] = fn.y; L.rayNrm[k][2][o] = fn.z;
+        }
     }
     const int rest = n - take;
-    const int moved = lane < rest ? L.hitQ[take + lane] : 0;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    if (lane < rest) L.hitQ[lane] = moved;
-    if (lane == 0) L.hitN = rest;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int moved = lane < rest ? L.candQ[take + lane] : 0;
+    waveSync();
+    if (lane < rest) L.candQ[lane] = moved;
+    if (lane == 0) L.candN = rest;
+    waveSync();
+}
+
+// after each screen round: drain full chunks; after the last, drain everything
+DI void contactDrain(const Dev& d, ContactLds& L, int lane, bool last)
+{
+    waveSync();
+    while (L.candN >= 64 || (last && L.candN > 0)) contactHeavy(d, L, lane);
 }
 
 // Owner side, before the search: pose, rays and (with sat) the plane points
 // of the car-arena search into LDS.
-DI void contactPrepare(ContactLds& L, int lane, bool sat, V3 cen, Q4 rot, int first)
+DI void contactPrepare(ContactLds& L, int lane, bool sat, V3 cen, Q4 rot, int first, bool screen)
 {
     const V3 dir = -rotate(rot, kZ);
     L.first[lane] = first;
     L.satOn[lane] = sat;
-    L.cen[0][lane] = cen.x; L.cen[1][lane] = cen.y; L.cen[2][lane] = cen.z;
     L.rot[0][lane] = rot.x; L.rot[1][lane] = rot.y; L.rot[2][lane] = rot.z; L.rot[3][lane] = rot.w;
-    L.dir[0][lane] = dir.x; L.dir[1][lane] = dir.y; L.dir[2][lane] = dir.z;
+    const V3 ax = rotate(rot, kX), ay = rotate(rot, kY), az = rotate(rot, kZ);
+    V3 lo{ kFltMax, kFltMax, kFltMax }, hi{ -kFltMax, -kFltMax, -kFltMax };
 #pragma unroll
     for (int k = 0; k < kWheels; k++) {
         const V3 st = wheelStart(cen, rot, k);
+        const V3 en = st + dir * (wheelRay(k) + 1.f);
+        lo = vmin(lo, vmin(st, en));
+        hi = vmax(hi, vmax(st, en));
         L.start[k][0][lane] = st.x; L.start[k][1][lane] = st.y; L.start[k][2][lane] = st.z;
         L.rayKey[k][lane] = kNoKey;
     }
+    const bool screened = screen && fabsf(cen.x) < kScreenRange && fabsf(cen.y) < kScreenRange &&
+                          fabsf(cen.z) < kScreenRange && qdot(rot, rot) > 0.25f;
+    L.scr[0][lane] = make_float4(cen.x, cen.y, cen.z, lo.x);
+    L.scr[1][lane] = make_float4(ax.x, ax.y, ax.z, lo.y);
+    L.scr[2][lane] = make_float4(ay.x, ay.y, ay.z, lo.z);
+    L.scr[3][lane] = make_float4(az.x, az.y, az.z, hi.x);
+    L.scr[4][lane] = make_float4(hi.y, hi.z, screened ? 1.f : 0.f, sat ? 1.f : 0.f);
     ManPt pts[kMaxManifold];
 #pragma unroll
     for (int i = 0; i < kMaxManifold; i++) pts[i] = ManPt{ kZero, kZero, kZero, 0.f };
@@ -1072,7 +1201,7 @@ DI void contactPrepare(ContactLds& L, int lane, bool sat, V3 cen, Q4 rot, int fi
     }
     L.satHits[lane] = 0;
     L.bestKey[lane] = kNoKey;
-    if (lane == 0) L.hitN = 0;
+    if (lane == 0) L.candN = 0;
 }
 
 // Owner side, after the search: wheel hits (arena winner, then cars and the
@@ -1090,18 +1219,9 @@ DI int contactFinish(const Dev& d, const ContactLds& L, int lane, int car, int s
         start[k] = wheelStart(cen, rot, k);
         const unsigned long long key = L.rayKey[k][lane];
         if (key == kNoKey) continue;
-        const Tri t = loadTri(d.arena, L.first[lane] + (int)(uint32_t)key);
         w.dist[k] = __uint_as_float((uint32_t)(key >> 32));
         w.src[k] = kSrcArena;
-        // arena triangles are non-degenerate (|e1 x e2|^2 > 1e-12 is checked
-        // when the mesh is built), so the winner always sets the normal
-        V3 fn = cross(t.e1, t.e2);
-        const float nl = lensq(fn);
-        if (nl > 1e-12f) {
-            fn = fn * rsqrt_(nl);
-            if (dot(fn, dir) > 0.f) fn = -fn;
-            w.normal[k] = fn;
-        }
+        w.normal[k] = V3{ L.rayNrm[k][0][lane], L.rayNrm[k][1][lane], L.rayNrm[k][2][lane] };
     }
     raycastBodies(d, car, sim, start, dir, w);
     const unsigned long long best = L.bestKey[lane];

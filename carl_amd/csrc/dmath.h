@@ -85,6 +85,7 @@ HDI V3 operator+(V3 a, float s) { return V3{ a.x + s, a.y + s, a.z + s }; }
 HDI V3 operator-(V3 a, float s) { return V3{ a.x - s, a.y - s, a.z - s }; }
 HDI V3 operator-(V3 a) { return V3{ -a.x, -a.y, -a.z }; }
 HDI V3 vabs(V3 a) { return V3{ fabsf(a.x), fabsf(a.y), fabsf(a.z) }; }
+HDI float l1norm(V3 a) { return (fabsf(a.x) + fabsf(a.y)) + fabsf(a.z); }
 HDI V3 vsign(V3 a) { return V3{ a.x >= 0.f ? 1.f : -1.f, a.y >= 0.f ? 1.f : -1.f, a.z >= 0.f ? 1.f : -1.f }; }
 HDI float dot(V3 a, V3 b) { return a.x * b.x + a.y * b.y + a.z * b.z; }
 HDI V3 cross(V3 a, V3 b) { return V3{ a.y * b.z - a.z * b.y, a.z * b.x - a.x * b.z, a.x * b.y - a.y * b.x }; }

@@ -70,7 +70,7 @@ struct SimRange {
 constexpr int kContactBlock = 64;
 constexpr int kContactOwners = 32;
 
-__global__ __launch_bounds__(kContactBlock) void contactKernel(Dev d, uint32_t* __restrict__ ws, SimRange range)
+__global__ __launch_bounds__(kContactBlock) void contactKernel(Dev d, uint32_t* __restrict__ ws, int screen, SimRange range)
 {
     __shared__ ContactLds L;
     const int lane = threadIdx.x;
@@ -86,15 +86,12 @@ __global__ __launch_bounds__(kContactBlock) void contactKernel(Dev d, uint32_t* 
         bp = broadphase(d, d.cv(CARL_CAR_POS, car), d.cv(CARL_CAR_VEL, car), d.cv(CARL_CAR_ANG, car), cen, rot);
         demoed = d.ci(CARL_CAR_DEMOED, car) != 0;
     }
-    contactPrepare(L, lane, ok && !demoed, cen, rot, bp.start);
+    contactPrepare(L, lane, ok && !demoed, cen, rot, bp.start, screen != 0);
     __syncthreads();
     waveItemsPipelined(
         bp.count, L.excl, [&](int o, int q, bool valid) { return contactFetch(d, L, o, q, valid); },
-        [&](const Tri& t, int o, int q, int base) { contactItem(d, L, t, o, q, base, lane); },
-        [&](bool last) {
-            contactFlush(d, L, lane, false);
-            if (last) contactFlush(d, L, lane, true);
-        });
+        [&](const RefBox& b, int o, int q, int) { contactScreen(L, b, o, q, lane); },
+        [&](bool last) { contactDrain(d, L, lane, last); });
     __syncthreads();
     if (!ok) return;
     Wheels w;
@@ -293,7 +290,7 @@ __global__ void setCarKernel(Dev d, const float* pos, const float* rot, const fl
 
 // Wheel contacts of the selected cars against the restored scene (rays only,
 // searched cooperatively like the contact kernel).  One wave per block.
-__global__ __launch_bounds__(kContactBlock) void refreshKernel(Dev d, Selection sel)
+__global__ __launch_bounds__(kContactBlock) void refreshKernel(Dev d, Selection sel, int screen)
 {
     __shared__ ContactLds L;
     const int lane = threadIdx.x;
@@ -312,11 +309,12 @@ __global__ __launch_bounds__(kContactBlock) void refreshKernel(Dev d, Selection 
         rot = d.cq(CARL_CAR_ROT, car);
         bp = broadphase(d, d.cv(CARL_CAR_POS, car), d.cv(CARL_CAR_VEL, car), d.cv(CARL_CAR_ANG, car), cen, rot);
     }
-    contactPrepare(L, lane, false, cen, rot, bp.start);
+    contactPrepare(L, lane, false, cen, rot, bp.start, screen != 0);
     __syncthreads();
     waveItemsPipelined(
         bp.count, L.excl, [&](int o, int q, bool valid) { return contactFetch(d, L, o, q, valid); },
-        [&](const Tri& t, int o, int q, int base) { contactItem(d, L, t, o, q, base, lane); });
+        [&](const RefBox& b, int o, int q, int) { contactScreen(L, b, o, q, lane); },
+        [&](bool last) { contactDrain(d, L, lane, last); });
     __syncthreads();
     if (car < 0) return;
     if (!active) {
@@ -442,6 +440,7 @@ struct carl_env {
     int* cellStart = nullptr;
     float4* angles = nullptr;
     float4* triRec = nullptr;
+    float4* refBox = nullptr;
     float *obs = nullptr, *tobs = nullptr, *state = nullptr, *tstate = nullptr, *rewards = nullptr;
     bool *dones = nullptr, *overtime = nullptr, *tovertime = nullptr;
     int32_t *score = nullptr, *ticks = nullptr, *tscore = nullptr, *tticks = nullptr;
@@ -449,6 +448,7 @@ struct carl_env {
     float* cactions = nullptr;
     uint32_t* ws = nullptr;  // per-tick car workspace (kWsPlanes planes)
     int tickStreams = kMaxTickStreams;   // partitions of the tick, one stream each
+    int contactScreen = 1;               // screen (car, triangle) pairs in the contact search
     hipStream_t aux[kMaxTickStreams - 1] = {};
     hipEvent_t fork = nullptr, join[kMaxTickStreams - 1] = {};
     bool timing = false;
@@ -461,7 +461,7 @@ struct carl_env {
     {
         Dev d;
         d.car = car; d.sim = sim; d.nSim = nSim; d.nBlue = nBlue; d.nCars = nCars; d.nTotal = nTotal; d.seed = seed;
-        d.arena = ArenaView{ rec, cellStart, angles, triRec };
+        d.arena = ArenaView{ rec, cellStart, angles, triRec, refBox };
         return d;
     }
     DoneRule rule() const { return DoneRule{ maxTicks, overtimeTicks, noTouchTicks }; }
@@ -480,7 +480,7 @@ int devAlloc(T** p, size_t count)
 
 void freeAll(carl_env* e)
 {
-    void* ptrs[] = { e->car, e->sim, e->rec, e->cellStart, e->angles, e->triRec, e->obs, e->tobs, e->state, e->tstate,
+    void* ptrs[] = { e->car, e->sim, e->rec, e->cellStart, e->angles, e->triRec, e->refBox, e->obs, e->tobs, e->state, e->tstate,
                      e->rewards, e->dones, e->overtime, e->tovertime, e->score, e->ticks, e->tscore, e->tticks,
                      e->actions, e->cactions, e->ws };
     for (void* p : ptrs)
@@ -544,7 +544,7 @@ int launchTicks(carl_env* e, int kind, const void* actions, int n)
             hipStream_t st = stream[p];
             const bool timed = p == 0;
             if (timed) CARL_MARK(CARL_KERNEL_CONTACT);
-            contactKernel<<<e->grid(cars, kContactOwners), kContactBlock, 0, st>>>(d, e->ws, r);
+            contactKernel<<<e->grid(cars, kContactOwners), kContactBlock, 0, st>>>(d, e->ws, e->contactScreen, r);
             if (timed) CARL_MARK(CARL_KERNEL_CAR_ARENA);
             carArenaKernel<<<e->grid(cars, kTickBlock), kTickBlock, 0, st>>>(d, e->ws, kind, actions, tick, r);
             if (timed) CARL_MARK(CARL_KERNEL_CAR_CAR);
@@ -639,7 +639,7 @@ int setCarRows(carl_env* e, const float* pos, const float* rot, const float* vel
     setCarKernel<<<e->grid(n, 256), 256, 0, e->stream>>>(e->dev(), pos, rot, vel, ang, demoed, byteDemoed, boost,
                                                           internal, sel);
     HIP_TRY(hipGetLastError());
-    refreshKernel<<<e->grid(n, kContactBlock), kContactBlock, 0, e->stream>>>(e->dev(), sel);
+    refreshKernel<<<e->grid(n, kContactBlock), kContactBlock, 0, e->stream>>>(e->dev(), sel, e->contactScreen);
     HIP_TRY(hipGetLastError());
     return CARL_OK;
 }
@@ -728,6 +728,7 @@ int carl_env_create(int nSim, int nBlue, int nOrange, int seed, int frameskip, i
     rc = rc ? rc : devAlloc(&e->cellStart, host.cellStart.size());
     rc = rc ? rc : devAlloc(&e->angles, host.angles.size() / 3);
     rc = rc ? rc : devAlloc(&e->triRec, host.triRecords.size() / 4);
+    rc = rc ? rc : devAlloc(&e->refBox, host.refBoxes.size() / 4);
     rc = rc ? rc : devAlloc(&e->obs, nT * e->obsDim);
     rc = rc ? rc : devAlloc(&e->tobs, nT * e->obsDim);
     rc = rc ? rc : devAlloc(&e->state, nS * e->stateDim);
@@ -753,6 +754,8 @@ int carl_env_create(int nSim, int nBlue, int nOrange, int seed, int frameskip, i
                != hipSuccess
         || hipMemcpy(e->angles, ang.data(), ang.size() * sizeof(float4), hipMemcpyHostToDevice) != hipSuccess
         || hipMemcpy(e->triRec, host.triRecords.data(), host.triRecords.size() * sizeof(float), hipMemcpyHostToDevice)
+               != hipSuccess
+        || hipMemcpy(e->refBox, host.refBoxes.data(), host.refBoxes.size() * sizeof(float), hipMemcpyHostToDevice)
                != hipSuccess)
         return bail(fail(CARL_ERR_RUNTIME, "arena upload failed"));
 
@@ -953,6 +956,10 @@ int carl_env_set_param(carl_env* e, int p, int v)
         if (v < 1 || v > kMaxTickStreams) return fail(CARL_ERR_VALUE, "tick_streams must be in [1, 4]");
         e->tickStreams = v;
         return CARL_OK;
+    case CARL_PARAM_CONTACT_SCREEN:
+        if (v != 0 && v != 1) return fail(CARL_ERR_VALUE, "contact_screen must be 0 or 1");
+        e->contactScreen = v;
+        return CARL_OK;
     default: return fail(CARL_ERR_VALUE, "parameter is read-only or unknown");
     }
 }
@@ -974,6 +981,7 @@ int carl_env_get_param(carl_env* e, int p, int* v)
     case CARL_PARAM_TICK_COUNT: *v = e->tickCount; break;
     case CARL_PARAM_N_BLUE: *v = e->nBlue; break;
     case CARL_PARAM_TICK_STREAMS: *v = e->tickStreams; break;
+    case CARL_PARAM_CONTACT_SCREEN: *v = e->contactScreen; break;
     default: return fail(CARL_ERR_VALUE, "unknown parameter");
     }
     return CARL_OK;

@@ -32,6 +32,7 @@ struct ArenaView {
     const int* cellStart;    // kCells + 1 offsets into rec (in references)
     const float4* angles;    // signed edge angles per triangle (xyz)
     const float4* tri;       // 4 per triangle, by triangle index (same record layout)
+    const float4* box;       // 4 per cell reference: contact-search screening data (arena.cpp)
 };
 
 struct Tri {

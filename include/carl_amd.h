@@ -109,8 +109,11 @@ enum {
     CARL_PARAM_STATE_DIM = 8,    /* read-only */
     CARL_PARAM_TICK_COUNT = 9,   /* read-only: global physics tick counter */
     CARL_PARAM_N_BLUE = 10,      /* read-only */
-    CARL_PARAM_TICK_STREAMS = 11 /* partitions of the simulations, each ticked on its own stream [1, 4];
-                                    no reference counterpart (default 4) */
+    CARL_PARAM_TICK_STREAMS = 11, /* partitions of the simulations, each ticked on its own stream [1, 4];
+                                     no reference counterpart (default 4) */
+    CARL_PARAM_CONTACT_SCREEN = 12 /* 1: the contact search drops (car, triangle) pairs its float tests
+                                      provably reject before running them; 0: it runs them on every pair.
+                                      Results are identical; no reference counterpart (default 1) */
 };
 
 /* ---- persistent state layout (export / import) ------------------------
