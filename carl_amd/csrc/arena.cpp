@@ -196,7 +196,7 @@ std::string buildArena(const std::string& objPath, HostArena& out)
     }
 
     // device records, per triangle and per cell reference
-    if (nTris > kMaxArenaTris) return "arena mesh has more than 65535 triangles";
+    if (nTris >= kMaxArenaTris) return "arena mesh has more than 2^24 triangles";
     out.triRecords.assign(16 * (size_t)nTris, 0.f);
     const int nRefs = out.cellStart[kCells];
     out.records.assign(16 * (size_t)nRefs, 0.f);
@@ -265,6 +265,52 @@ std::string buildArena(const std::string& objPath, HostArena& out)
                               (float)(nz / nl), (float)((nx * ax + ny * ay + nz * az) / nl), (float)rayCond, (float)rayTol,
                               (float)s1, (float)s2, (float)s3, (float)epsEdge };
         std::memcpy(&screen[16 * (size_t)t], f, sizeof f);
+    }
+    // ball candidate grid.  A ball only tests triangles registered in the
+    // broadphase cells its box overlaps; each reference carries the
+    // triangle's edge angles and its registration range (x0 x1 y0 y1 6 bits
+    // each, z0 z1 4 bits) so the ball can apply that rule itself.
+    {
+        const double reach = (double)kBallRadius + (double)kBallArenaBreak + 1.0;
+        auto fineRange = [&](int t, int (&a)[3], int (&b)[3]) {
+            const double l[3] = { lo[t].x, lo[t].y, lo[t].z }, h[3] = { hi[t].x, hi[t].y, hi[t].z };
+            const double o[3] = { kArenaMin.x, kArenaMin.y, kArenaMin.z };
+            const int n[3] = { kFineX, kFineY, kFineZ };
+            for (int k = 0; k < 3; k++) {
+                a[k] = std::max(0, (int)std::floor((l[k] - reach - o[k]) / kFineCell));
+                b[k] = std::min(n[k] - 1, (int)std::floor((h[k] + reach - o[k]) / kFineCell));
+            }
+        };
+        std::vector<int> fcount(kFineCells + 1, 0);
+        for (int t = 0; t < nTris; t++) {
+            int a[3], b[3];
+            fineRange(t, a, b);
+            for (int z = a[2]; z <= b[2]; z++)
+                for (int y = a[1]; y <= b[1]; y++)
+                    for (int x = a[0]; x <= b[0]; x++) fcount[x + kFineX * (y + kFineY * z)]++;
+        }
+        out.fineStart.assign(kFineCells + 1, 0);
+        for (int c = 0; c < kFineCells; c++) out.fineStart[c + 1] = out.fineStart[c] + fcount[c];
+        const size_t nFine = (size_t)out.fineStart[kFineCells];
+        out.fineRecords.assign(16 * nFine, 0.f);
+        out.fineAux.assign(4 * nFine, 0.f);
+        std::fill(fcount.begin(), fcount.end(), 0);
+        for (int t = 0; t < nTris; t++) {
+            int a[3], b[3];
+            fineRange(t, a, b);
+            const auto& r = range[t];
+            const uint32_t reg = (uint32_t)r[0] | (uint32_t)r[3] << 6 | (uint32_t)r[1] << 12 | (uint32_t)r[4] << 18 |
+                                 (uint32_t)r[2] << 24 | (uint32_t)r[5] << 28;
+            for (int z = a[2]; z <= b[2]; z++)
+                for (int y = a[1]; y <= b[1]; y++)
+                    for (int x = a[0]; x <= b[0]; x++) {
+                        const int c = x + kFineX * (y + kFineY * z);
+                        const size_t f = (size_t)out.fineStart[c] + fcount[c]++;
+                        std::memcpy(&out.fineRecords[16 * f], &out.triRecords[16 * (size_t)t], 16 * sizeof(float));
+                        std::memcpy(&out.fineAux[4 * f], &out.angles[3 * (size_t)t], 3 * sizeof(float));
+                        std::memcpy(&out.fineAux[4 * f + 3], &reg, sizeof reg);
+                    }
+        }
     }
     out.refBoxes.assign(16 * (size_t)nRefs, 0.f);
     for (int r = 0; r < nRefs; r++) {

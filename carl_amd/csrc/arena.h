@@ -1,6 +1,7 @@
 // arena.h - host-side construction of the soccar collision mesh.
 #pragma once
 
+#include <cstdint>
 #include <string>
 #include <vector>
 
@@ -16,6 +17,9 @@ struct HostArena {
     std::vector<float> records;     // 16 floats per cell reference (device layout, see state.h)
     std::vector<float> triRecords;  // the same 16 floats per triangle, by triangle index
     std::vector<float> refBoxes;    // 16 floats per cell reference: contact-search screening data
+    std::vector<int> fineStart;     // kFineCells + 1 offsets into fineRecords (in references)
+    std::vector<float> fineRecords; // 16 floats per ball-grid reference (record layout), ascending per cell
+    std::vector<float> fineAux;     // 4 per ball-grid reference: edge angles xyz, registration range (bits)
 };
 
 // Parse, weld and index the mesh.  Returns "" on success, else the error text.

@@ -26,6 +26,14 @@ constexpr float kCellX = (kArenaMax.x - kArenaMin.x) / 48.f;
 constexpr float kCellY = (kArenaMax.y - kArenaMin.y) / 48.f;
 constexpr float kCellZ = (kArenaMax.z - kArenaMin.z) / 10.f;
 constexpr float kBoundaryEdge = 2.f * kPi;
+// ball candidate grid: cubic cells over the broadphase box; a cell lists every
+// triangle whose box comes within ball reach (+1 uu) of the cell
+constexpr float kFineCell = 128.f;
+constexpr int kFineX = 65, kFineY = 94, kFineZ = 17;   // ceil(extent / kFineCell)
+constexpr int kFineCells = kFineX * kFineY * kFineZ;
+static_assert(kFineX * kFineCell >= kArenaMax.x - kArenaMin.x && kFineY * kFineCell >= kArenaMax.y - kArenaMin.y &&
+                  kFineZ * kFineCell >= kArenaMax.z - kArenaMin.z,
+              "ball grid must cover the broadphase box");
 
 // car
 constexpr V3 kHalf{ 60.186455f, 43.282655f, 19.262505f };

@@ -164,38 +164,50 @@ constexpr int kBallOwners = 32;
 
 __global__ __launch_bounds__(kBallBlock) void ballKernel(Dev d, int tick, SimRange range)
 {
-    __shared__ BallGatherLds L;
+    __shared__ BallLds L;
     const int lane = threadIdx.x;
     const int sim = range.begin + blockIdx.x * kBallOwners + lane;
     const bool ok = lane < kBallOwners && sim < range.end;
     const bool awake = ok && !ballSleeping(d, sim);
     const V3 center = ok ? d.sv(CARL_SIM_BALL_POS, sim) : kZero;
-    int items = 0;
+    int items = 0, first = 0, cell = 0;
     bool sequential = false;
     if (awake) {
-        items = ballGatherRuns(d, center, L, lane);
-        if (items < 0) {
+        if (ballGridCell(center, cell)) {
+            first = d.arena.fineStart[cell];
+            items = d.arena.fineStart[cell + 1] - first;
+        } else {
             sequential = true;
-            items = 0;
         }
     }
-    L.cx[lane] = center.x;
-    L.cy[lane] = center.y;
-    L.cz[lane] = center.z;
-    L.hitN[lane] = 0;
-    if (!awake || sequential) L.runs[lane] = 0;
+    ballPrepare(L, lane, center, first);
     __syncthreads();
+    BallContact cs[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) cs[k] = BallContact{ kZero, kZero, kZero, 0.f, kZero };
+    int count = 0;
+    bool hit = false;
+    int roundBase = 0;
     waveItemsPipelined(
         items, L.excl, [&](int o, int q, bool valid) { return ballGatherFetch(d, L, o, q, valid); },
-        [&](const BallItem& item, int o, int, int) { ballGatherItem(L, item, o); });
-    __syncthreads();
+        [&](const BallItem& item, int o, int, int) { hit = ballGatherItem(L, item, o, lane); },
+        [&](bool) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            const unsigned long long hits = __ballot(hit);
+            hit = false;
+            if (items > 0) {
+                const int a = L.excl[lane] - roundBase, b = L.excl[lane] + items - roundBase;
+                if (b > 0 && a < 64) foldStashedContacts(L, hits, a > 0 ? a : 0, b < 64 ? b : 64, cs, count);
+            }
+            roundBase += 64;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        });
     if (!ok) return;
-    BallContact cs[4];
-    int count = 0;
-    if (awake) {
-        if (sequential || L.hitN[lane] > kBallHits) count = gatherBallContacts(d, center, cs);
-        else count = ballContactsFromHits(d, center, L, lane, cs);
-    }
+    if (sequential) count = gatherBallContacts(d, center, cs);
     ballTick(d, sim, tick, cs, count);
 }
 
@@ -441,6 +453,9 @@ struct carl_env {
     float4* angles = nullptr;
     float4* triRec = nullptr;
     float4* refBox = nullptr;
+    float4* fineRec = nullptr;
+    float4* fineAux = nullptr;
+    int* fineStart = nullptr;
     float *obs = nullptr, *tobs = nullptr, *state = nullptr, *tstate = nullptr, *rewards = nullptr;
     bool *dones = nullptr, *overtime = nullptr, *tovertime = nullptr;
     int32_t *score = nullptr, *ticks = nullptr, *tscore = nullptr, *tticks = nullptr;
@@ -461,7 +476,7 @@ struct carl_env {
     {
         Dev d;
         d.car = car; d.sim = sim; d.nSim = nSim; d.nBlue = nBlue; d.nCars = nCars; d.nTotal = nTotal; d.seed = seed;
-        d.arena = ArenaView{ rec, cellStart, angles, triRec, refBox };
+        d.arena = ArenaView{ rec, cellStart, angles, triRec, refBox, fineRec, fineAux, fineStart };
         return d;
     }
     DoneRule rule() const { return DoneRule{ maxTicks, overtimeTicks, noTouchTicks }; }
@@ -480,9 +495,10 @@ int devAlloc(T** p, size_t count)
 
 void freeAll(carl_env* e)
 {
-    void* ptrs[] = { e->car, e->sim, e->rec, e->cellStart, e->angles, e->triRec, e->refBox, e->obs, e->tobs, e->state, e->tstate,
-                     e->rewards, e->dones, e->overtime, e->tovertime, e->score, e->ticks, e->tscore, e->tticks,
-                     e->actions, e->cactions, e->ws };
+    void* ptrs[] = { e->car, e->sim, e->rec, e->cellStart, e->angles, e->triRec, e->refBox, e->fineRec,
+                     e->fineAux, e->fineStart, e->obs, e->tobs, e->state, e->tstate, e->rewards, e->dones,
+                     e->overtime, e->tovertime, e->score, e->ticks, e->tscore, e->tticks, e->actions, e->cactions,
+                     e->ws };
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
     for (hipEvent_t ev : e->marks) (void)hipEventDestroy(ev);
@@ -729,6 +745,9 @@ int carl_env_create(int nSim, int nBlue, int nOrange, int seed, int frameskip, i
     rc = rc ? rc : devAlloc(&e->angles, host.angles.size() / 3);
     rc = rc ? rc : devAlloc(&e->triRec, host.triRecords.size() / 4);
     rc = rc ? rc : devAlloc(&e->refBox, host.refBoxes.size() / 4);
+    rc = rc ? rc : devAlloc(&e->fineRec, host.fineRecords.size() / 4);
+    rc = rc ? rc : devAlloc(&e->fineAux, host.fineAux.size() / 4);
+    rc = rc ? rc : devAlloc(&e->fineStart, host.fineStart.size());
     rc = rc ? rc : devAlloc(&e->obs, nT * e->obsDim);
     rc = rc ? rc : devAlloc(&e->tobs, nT * e->obsDim);
     rc = rc ? rc : devAlloc(&e->state, nS * e->stateDim);
@@ -756,6 +775,12 @@ int carl_env_create(int nSim, int nBlue, int nOrange, int seed, int frameskip, i
         || hipMemcpy(e->triRec, host.triRecords.data(), host.triRecords.size() * sizeof(float), hipMemcpyHostToDevice)
                != hipSuccess
         || hipMemcpy(e->refBox, host.refBoxes.data(), host.refBoxes.size() * sizeof(float), hipMemcpyHostToDevice)
+               != hipSuccess
+        || hipMemcpy(e->fineRec, host.fineRecords.data(), host.fineRecords.size() * sizeof(float),
+                     hipMemcpyHostToDevice) != hipSuccess
+        || hipMemcpy(e->fineAux, host.fineAux.data(), host.fineAux.size() * sizeof(float), hipMemcpyHostToDevice)
+               != hipSuccess
+        || hipMemcpy(e->fineStart, host.fineStart.data(), host.fineStart.size() * sizeof(int), hipMemcpyHostToDevice)
                != hipSuccess)
         return bail(fail(CARL_ERR_RUNTIME, "arena upload failed"));
 

@@ -569,121 +569,117 @@ DI int gatherBallContacts(const Dev& d, V3 center, BallContact* cs)
     }
 }
 
-// ---- cooperative gather: one wave gathers the arena contacts of 64 balls.
-// The cell runs of every ball are flattened over the wave (waveItems); each
-// item is tested with the same conservative box and exact sphere test as the
-// sequential path, and passing triangles are appended to the owner's list.
-// A triangle registered in several of the ball's cells is taken only in the
-// first of them (the low corner of the overlap of its registration box with
-// the ball's cell box), so every list holds distinct triangles.  The owner
-// then sorts its list by triangle index and reduces the contacts in that
-// order, which is exactly what the sequential merge produces: triangles that
-// fail the sphere test add nothing there either.
-constexpr int kBallCells = 12;  // a 186.3 uu box spans at most 3 x 2 x 2 cells
-constexpr int kBallHits = 128;  // distinct triangles within reach (more than 64 seen at the goal posts)
-
-struct BallGatherLds {
+// ---- cooperative gather over the ball candidate grid.  A ball's candidates
+// are the list of the grid cell holding its centre: every triangle whose box
+// comes within reach + 1 uu of that cell, each once, in ascending triangle
+// order.  The reference tests the triangles registered in the broadphase cells
+// its box overlaps, merged in ascending index order, so an item counts only
+// when its registration range meets the ball's cell box; then the same
+// sphere test decides.  A triangle the list leaves out lies more than
+// reach + 1 from the centre, where the sphere test fails: its closest point is
+// a convex combination of the vertices, rounded far below 1 uu.  The lists of
+// the wave's balls are walked by all 64 lanes (waveItemsPipelined); each
+// round's contacts are stashed in LDS and every owner folds its own, in list
+// order, into its reduced set (BallArena/Contact.cuh:513-594).
+struct BallLds {
     int excl[64];
-    int runs[64];
-    int runStart[kBallCells][64];
-    int runFirst[kBallCells][64];
-    int runCell[kBallCells][64];
-    int lo[3][64];
+    int first[64];                  // the owner's first grid reference
+    int cellLo[3][64], cellHi[3][64];  // the ball's broadphase cell box
     float cx[64], cy[64], cz[64];
-    int hitN[64];
-    unsigned short hitIdx[kBallHits][64];  // triangle indices (< kMaxArenaTris)
+    float stash[13][64];            // this round's contacts, by lane
 };
 
-// Cell runs of one ball into the owner's LDS slots; returns the item count,
-// or -1 when the runs do not fit (the sequential path then gathers).
-DI int ballGatherRuns(const Dev& d, V3 center, BallGatherLds& L, int lane)
+// grid cell of a ball centre; false outside the grid (the sequential gather
+// then serves the ball)
+DI bool ballGridCell(V3 c, int& cell)
+{
+    const float x = (c.x - kArenaMin.x) / kFineCell;
+    const float y = (c.y - kArenaMin.y) / kFineCell;
+    const float z = (c.z - kArenaMin.z) / kFineCell;
+    if (!(x >= 0.f && x < (float)kFineX && y >= 0.f && y < (float)kFineY && z >= 0.f && z < (float)kFineZ))
+        return false;
+    cell = (int)x + kFineX * ((int)y + kFineY * (int)z);
+    return true;
+}
+
+DI void ballPrepare(BallLds& L, int lane, V3 center, int first)
 {
     const float ext = kBallRadius + kBallArenaBreak;
     int lo[3], hi[3];
     cellOf(center - ext, lo[0], lo[1], lo[2]);
     cellOf(center + ext, hi[0], hi[1], hi[2]);
-    int runs = 0, count = 0;
-    for (int z = lo[2]; z <= hi[2]; z++)
-        for (int y = lo[1]; y <= hi[1]; y++)
-            for (int x = lo[0]; x <= hi[0]; x++) {
-                const int cell = flatCell(x, y, z);
-                const int s = d.arena.cellStart[cell], e = d.arena.cellStart[cell + 1];
-                if (e == s) continue;
-                if (runs == kBallCells) return -1;
-                L.runStart[runs][lane] = s;
-                L.runFirst[runs][lane] = count;
-                L.runCell[runs][lane] = cell;
-                runs++;
-                count += e - s;
-            }
-    L.runs[lane] = runs;
-    L.lo[0][lane] = lo[0];
-    L.lo[1][lane] = lo[1];
-    L.lo[2][lane] = lo[2];
-    return count;
+#pragma unroll
+    for (int k = 0; k < 3; k++) {
+        L.cellLo[k][lane] = lo[k];
+        L.cellHi[k][lane] = hi[k];
+    }
+    L.cx[lane] = center.x;
+    L.cy[lane] = center.y;
+    L.cz[lane] = center.z;
+    L.first[lane] = first;
 }
 
 struct BallItem {
     Tri t;
-    int run;  // which of the owner's cell runs the triangle came from
+    float4 aux;   // signed edge angles xyz, packed registration range (bits)
 };
 
 // the triangle of item q of owner o (reference 0 for lanes without an item)
-DI BallItem ballGatherFetch(const Dev& d, const BallGatherLds& L, int o, int q, bool valid)
+DI BallItem ballGatherFetch(const Dev& d, const BallLds& L, int o, int q, bool valid)
 {
-    int r = 0, ref = 0;
-    if (valid) {
-        const int nr = L.runs[o];
-        while (r + 1 < nr && L.runFirst[r + 1][o] <= q) r++;
-        ref = L.runStart[r][o] + (q - L.runFirst[r][o]);
-    }
-    return BallItem{ loadTri(d.arena, ref), r };
+    const int ref = valid ? L.first[o] + q : 0;
+    return BallItem{ unpackTri(d.arena.fineRec + 4 * (size_t)ref), d.arena.fineAux[ref] };
 }
 
-DI void ballGatherItem(BallGatherLds& L, const BallItem& item, int o)
+// Test one item; a contact is stashed at the lane's slot (true when there is one).
+DI bool ballGatherItem(BallLds& L, const BallItem& item, int o, int lane)
 {
     const Tri& t = item.t;
-    const int r = item.run;
+    const uint32_t r = __float_as_uint(item.aux.w);
+    if ((int)(r & 63) > L.cellHi[0][o] || (int)((r >> 6) & 63) < L.cellLo[0][o] ||
+        (int)((r >> 12) & 63) > L.cellHi[1][o] || (int)((r >> 18) & 63) < L.cellLo[1][o] ||
+        (int)((r >> 24) & 15) > L.cellHi[2][o] || (int)(r >> 28) < L.cellLo[2][o])
+        return false;
     const V3 center{ L.cx[o], L.cy[o], L.cz[o] };
     const float reach = kBallRadius + kBallArenaBreak + 1.f;
     const V3 mn = vmin(vmin(t.v0, t.v1), t.v2);
     const V3 mx = vmax(vmax(t.v0, t.v1), t.v2);
     if (center.x < mn.x - reach || center.x > mx.x + reach || center.y < mn.y - reach || center.y > mx.y + reach ||
         center.z < mn.z - reach || center.z > mx.z + reach)
-        return;
-    // first registration cell of this triangle inside the ball's cell box
-    // (registration spans [cell(min) - 1, cell(max)] per axis, clamped at 0)
-    int rx, ry, rz;
-    cellOf(mn, rx, ry, rz);
-    rx = rx - 1 < 0 ? 0 : rx - 1;
-    ry = ry - 1 < 0 ? 0 : ry - 1;
-    rz = rz - 1 < 0 ? 0 : rz - 1;
-    const int fx = rx > L.lo[0][o] ? rx : L.lo[0][o];
-    const int fy = ry > L.lo[1][o] ? ry : L.lo[1][o];
-    const int fz = rz > L.lo[2][o] ? rz : L.lo[2][o];
-    if (flatCell(fx, fy, fz) != L.runCell[r][o]) return;
+        return false;
     BallContact ct;
-    if (!sphereTriangle(center, t.v0, t.v1, t.v2, ct)) return;
-    const int slot = atomicAdd(&L.hitN[o], 1);
-    if (slot < kBallHits) L.hitIdx[slot][o] = (unsigned short)t.idx;
+    if (!sphereTriangle(center, t.v0, t.v1, t.v2, ct)) return false;
+    adjustBallEdge(ct, t.v0, t.v1, t.v2, V3{ item.aux.x, item.aux.y, item.aux.z });
+    ct.point = (center + ct.relPos) + ct.normal * ct.depth;
+    const float v[13] = { ct.point.x,  ct.point.y,  ct.point.z,  ct.relPos.x,    ct.relPos.y,    ct.relPos.z,   ct.normal.x,
+                          ct.normal.y, ct.normal.z, ct.depth,    ct.reduction.x, ct.reduction.y, ct.reduction.z };
+#pragma unroll
+    for (int i = 0; i < 13; i++) L.stash[i][lane] = v[i];
+    return true;
 }
 
-// Owner side: reduction of the gathered (distinct) hits in triangle order.
-DI int ballContactsFromHits(const Dev& d, V3 center, BallGatherLds& L, int lane, BallContact* cs)
+// Fold the stashed contacts of lanes [a, b) marked in `hits` into the set.
+DI void foldStashedContacts(const BallLds& L, unsigned long long hits, int a, int b, BallContact* cs, int& count)
 {
-    const int n = L.hitN[lane];
-    for (int i = 1; i < n; i++) {
-        const unsigned short key = L.hitIdx[i][lane];
-        int j = i - 1;
-        while (j >= 0 && L.hitIdx[j][lane] > key) {
-            L.hitIdx[j + 1][lane] = L.hitIdx[j][lane];
-            j--;
-        }
-        L.hitIdx[j + 1][lane] = key;
+    const unsigned long long hiMask = b >= 64 ? ~0ull : ((1ull << b) - 1);
+    unsigned long long bits = hits & hiMask & (~0ull << a);
+    while (bits) {
+        const int i = (int)__builtin_ctzll(bits);
+        bits &= bits - 1;
+        BallContact ct;
+        ct.point = V3{ L.stash[0][i], L.stash[1][i], L.stash[2][i] };
+        ct.relPos = V3{ L.stash[3][i], L.stash[4][i], L.stash[5][i] };
+        ct.normal = V3{ L.stash[6][i], L.stash[7][i], L.stash[8][i] };
+        ct.depth = L.stash[9][i];
+        ct.reduction = V3{ L.stash[10][i], L.stash[11][i], L.stash[12][i] };
+        // the edge adjustment changes only the normal, so the replacement
+        // choice sees what the reference's sees
+        int slot;
+        if (count < 4) slot = count++;
+        else slot = ballReplacement(cs, ct);
+#pragma unroll
+        for (int k = 0; k < 4; k++) cs[k] = sel(k == slot, ct, cs[k]);
     }
-    int count = 0;
-    for (int i = 0; i < n; i++) reduceBallContact(d, center, loadTriIdx(d.arena, L.hitIdx[i][lane]), cs, count);
-    return count;
 }
 
 struct BallBody {

@@ -25,7 +25,7 @@ namespace carl {
 
 constexpr uint32_t kPlaneFlag = 0x80000000u;  // analytic plane triangle: skipped by the car SAT
 
-constexpr int kMaxArenaTris = 65535;  // triangle indices are kept in 16 bits in LDS lists
+constexpr int kMaxArenaTris = 1 << 24;  // contact-search queue entries keep a run position in 24 bits
 
 struct ArenaView {
     const float4* rec;       // 4 per cell reference
@@ -33,6 +33,9 @@ struct ArenaView {
     const float4* angles;    // signed edge angles per triangle (xyz)
     const float4* tri;       // 4 per triangle, by triangle index (same record layout)
     const float4* box;       // 4 per cell reference: contact-search screening data (arena.cpp)
+    const float4* fineRec;   // 4 per ball-grid reference (record layout)
+    const float4* fineAux;   // per ball-grid reference: edge angles xyz, packed broadphase registration range
+    const int* fineStart;    // kFineCells + 1 offsets into fineRec (in references)
 };
 
 struct Tri {
