@@ -313,8 +313,10 @@ std::string buildArena(const std::string& objPath, HostArena& out)
         }
     }
     out.refBoxes.assign(16 * (size_t)nRefs, 0.f);
+    out.refAngles.assign(4 * (size_t)nRefs, 0.f);
     for (int r = 0; r < nRefs; r++) {
         const int t = out.cellTris[r];
+        std::memcpy(&out.refAngles[4 * (size_t)r], &out.angles[3 * (size_t)t], 3 * sizeof(float));
         std::memcpy(&out.records[16 * (size_t)r], &out.triRecords[16 * (size_t)t], 16 * sizeof(float));
         std::memcpy(&out.refBoxes[16 * (size_t)r], &screen[16 * (size_t)t], 16 * sizeof(float));
     }

@@ -17,6 +17,7 @@ struct HostArena {
     std::vector<float> records;     // 16 floats per cell reference (device layout, see state.h)
     std::vector<float> triRecords;  // the same 16 floats per triangle, by triangle index
     std::vector<float> refBoxes;    // 16 floats per cell reference: contact-search screening data
+    std::vector<float> refAngles;   // 4 per cell reference: the triangle's signed edge angles xyz, 0
     std::vector<int> fineStart;     // kFineCells + 1 offsets into fineRecords (in references)
     std::vector<float> fineRecords; // 16 floats per ball-grid reference (record layout), ascending per cell
     std::vector<float> fineAux;     // 4 per ball-grid reference: edge angles xyz, registration range (bits)

@@ -909,36 +909,26 @@ DI unsigned long long contactKey(float value, int item)
 // bestRef is the cell reference holding the deepest contact (found by the
 // cooperative search of the contact kernel), -1 for none; its contact is
 // regenerated here exactly as the search produced it.
-DI int buildManifold(const Dev& d, V3 cen, Q4 rot, int bestRef, ManPt* pts)
+// The car-arena manifold: the analytic plane points, then the deepest
+// triangle contact found by the contact search (Manifold.cuh; the search
+// hands over the point exactly as it would be regenerated from its triangle).
+DI int buildManifold(V3 cen, Q4 rot, bool hasBest, const ManPt& best, ManPt* pts)
 {
     int n = planeManifold(cen, rot, pts);
-    if (bestRef < 0) return n;
-    V3 near[kMaxManifold];
-#pragma unroll
-    for (int i = 0; i < kMaxManifold; i++) near[i] = pts[i].carPos;
-    const Tri tri = loadTri(d.arena, bestRef);
-    const LocalTri t = toLocal(tri, cen, rot);
-    const Sat s = boxTriSat(t);
-    Contact best{};
-    float bestVal = kFltMax;
-    if (!s.overlap || !triBestContact(t, s, near, n, best, bestVal)) return n;
-    const float4 ang = d.arena.angles[tri.idx];
-    adjustEdgeContact(t, V3{ ang.x, ang.y, ang.z }, best);
-    addManifold(pts, n, ManPt{ best.carPos, cen + rotate(rot, best.arenaPos), rotate(rot, best.normal), -best.depth });
+    if (hasBest) addManifold(pts, n, best);
     return n;
 }
 
 // ------------------------------------------------ cooperative cell search
 //
-// One wave searches the cell runs of its cars together, in three stages that
+// One wave searches the cell runs of its cars together, in two stages that
 // each keep all 64 lanes busy:
 //   screen every (car, cell triangle) item against bounds that prove the
 //          float tests of the next stage reject it; the others are queued in
 //          run order;
 //   heavy  queued items, 64 at a time: the four suspension rays and the
 //          box-triangle SAT; SAT hits are ranked in run order and the first
-//          kMaxTriHits of each car are queued;
-//   clip   queued hits, 64 at a time: contact generation.
+//          kMaxTriHits of each car generate their contacts.
 // Per wheel the nearest ray hit is kept by an LDS atomic minimum of
 // (distance, position in the run): the sequential walk keeps strictly nearer
 // hits, so this is its result.  Contacts compete by contactKey, whose minimum
@@ -984,6 +974,7 @@ struct ContactLds {
     unsigned long long rayKey[kWheels][64];
     unsigned long long bestKey[64];
     float rayNrm[kWheels][3][64];   // surface normal of each wheel's nearest arena hit
+    float bestPt[10][64];           // manifold point of the deepest arena contact so far
     // screened items in run order, entries owner << 24 | item
     int candQ[128];
     int candN;
@@ -1077,6 +1068,8 @@ DI void contactHeavy(const Dev& d, ContactLds& L, int lane)
     const int o = e >> 24, q = e & 0xffffff;
     bool rayHit = false;
     V3 fn = kZero;   // surface normal facing against the rays, for lanes with a ray hit
+    bool hasContact = false;
+    ManPt manPt{};   // this lane's contact as a manifold point
     if (active) {
         const Tri t = loadTri(d.arena, L.first[o] + q);
         const V3 dir = ownerDir(L, o);
@@ -1136,7 +1129,14 @@ DI void contactHeavy(const Dev& d, ContactLds& L, int lane)
                 near[i] = V3{ L.nearPos[i][0][o], L.nearPos[i][1][o], L.nearPos[i][2][o] };
             Contact c;
             float value = kFltMax;
-            if (triBestContact(lt, sat, near, L.nearN[o], c, value)) atomicMin(&L.bestKey[o], contactKey(value, q));
+            if (triBestContact(lt, sat, near, L.nearN[o], c, value)) {
+                atomicMin(&L.bestKey[o], contactKey(value, q));
+                const Q4 rot{ L.rot[0][o], L.rot[1][o], L.rot[2][o], L.rot[3][o] };
+                const float4 ang = d.arena.refAng[L.first[o] + q];
+                adjustEdgeContact(lt, V3{ ang.x, ang.y, ang.z }, c);
+                manPt = ManPt{ c.carPos, ownerCen(L, o) + rotate(rot, c.arenaPos), rotate(rot, c.normal), -c.depth };
+                hasContact = true;
+            }
         }
     }
     waveSync();
@@ -1148,6 +1148,14 @@ DI void contactHeavy(const Dev& d, ContactLds& L, int lane)
             if ((uint32_t)L.rayKey[k][o] != (uint32_t)q) continue;
             L.rayNrm[k][0][o] = fn.x; L.rayNrm[k][1][o] = fn.y; L.rayNrm[k][2][o] = fn.z;
         }
+    }
+    // likewise the lane holding the deepest contact so far
+    if (hasContact && (uint32_t)L.bestKey[o] == (uint32_t)q) {
+        const float v[10] = { manPt.carPos.x,      manPt.carPos.y,      manPt.carPos.z,      manPt.worldPos.x,
+                              manPt.worldPos.y,    manPt.worldPos.z,    manPt.worldNormal.x, manPt.worldNormal.y,
+                              manPt.worldNormal.z, manPt.dist };
+#pragma unroll
+        for (int i = 0; i < 10; i++) L.bestPt[i][o] = v[i];
     }
     const int rest = n - take;
     const int moved = lane < rest ? L.candQ[take + lane] : 0;
@@ -1510,14 +1518,14 @@ DI void solveManifold(Body& b, const ManPt* pts, int count)
 }
 
 // suspension, manifold and contact solve of one non-demoed car (Solve.cuh:286-314)
-DI void solveCarArena(const Dev& d, CarRegs& r, const Wheels& w, int bestRef, int tick)
+DI void solveCarArena(CarRegs& r, const Wheels& w, bool hasBest, const ManPt& best, int tick)
 {
     Body b = makeBody(r.pos, r.vel, r.ang, r.cen, r.rot);
     applySuspension(b, r, w, tick);
     ManPt pts[kMaxManifold];
 #pragma unroll
     for (int i = 0; i < kMaxManifold; i++) pts[i] = ManPt{ kZero, kZero, kZero, 0.f };
-    const int count = buildManifold(d, r.cen, r.rot, bestRef, pts);
+    const int count = buildManifold(r.cen, r.rot, hasBest, best, pts);
     if (count > 0) {
         solveManifold(b, pts, count);
         if (!(lensq(b.pushVel) == 0.f && lensq(b.turnVel) == 0.f))

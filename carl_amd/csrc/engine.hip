@@ -52,7 +52,10 @@ constexpr int kMaxTickStreams = 4;
 // Per-tick car workspace between the contact and the car-arena kernels, one
 // plane of nTotal 32-bit words each: wheel hit distance, normal xyz and
 // source per wheel, then the cell reference of the deepest arena contact.
-enum : int { kWsDist = 0, kWsNx = 4, kWsNy = 8, kWsNz = 12, kWsSrc = 16, kWsBest = 20, kWsPlanes = 21 };
+// kWsBest: cell reference of the deepest arena contact (-1: none); kWsMan:
+// that contact as a manifold point (car-local point xyz, world point xyz,
+// world normal xyz, signed distance)
+enum : int { kWsDist = 0, kWsNx = 4, kWsNy = 8, kWsNz = 12, kWsSrc = 16, kWsBest = 20, kWsMan = 21, kWsPlanes = 31 };
 
 // Simulations [begin, end) of one launch: the tick runs as independent
 // partitions on separate streams so the tail of one partition's kernel
@@ -106,6 +109,10 @@ __global__ __launch_bounds__(kContactBlock) void contactKernel(Dev d, uint32_t* 
         ws[(kWsSrc + k) * n + car] = (uint32_t)w.src[k];
     }
     ws[kWsBest * n + car] = (uint32_t)best;
+    if (best >= 0) {
+#pragma unroll
+        for (int i = 0; i < 10; i++) ws[(kWsMan + i) * n + car] = __float_as_uint(L.bestPt[i][lane]);
+    }
 }
 
 // A2: controls, car-arena contacts, suspension and the contact solve.
@@ -126,6 +133,13 @@ __global__ __launch_bounds__(kTickBlock, 2) void carArenaKernel(Dev d, const uin
         w.src[k] = (int)ws[(kWsSrc + k) * n + car];
     }
     const int best = (int)ws[kWsBest * n + car];
+    ManPt bestPt{};
+    if (best >= 0) {
+        float v[10];
+#pragma unroll
+        for (int i = 0; i < 10; i++) v[i] = __uint_as_float(ws[(kWsMan + i) * n + car]);
+        bestPt = ManPt{ V3{ v[0], v[1], v[2] }, V3{ v[3], v[4], v[5] }, V3{ v[6], v[7], v[8] }, v[9] };
+    }
     const Controls ctl = decodeControls(kind, actions, car);
     storeWheelOutputs(d, car, w);
     d.setf(CARL_CAR_CTRL_THROTTLE, car, ctl.throttle);
@@ -140,7 +154,7 @@ __global__ __launch_bounds__(kTickBlock, 2) void carArenaKernel(Dev d, const uin
     CarRegs r;
     loadRegs(d, car, r);
     applyControls(r, ctl, w);
-    solveCarArena(d, r, w, best, tick);
+    solveCarArena(r, w, best >= 0, bestPt, tick);
     storeRegs(d, car, r);
 }
 
@@ -453,6 +467,7 @@ struct carl_env {
     float4* angles = nullptr;
     float4* triRec = nullptr;
     float4* refBox = nullptr;
+    float4* refAng = nullptr;
     float4* fineRec = nullptr;
     float4* fineAux = nullptr;
     int* fineStart = nullptr;
@@ -476,7 +491,7 @@ struct carl_env {
     {
         Dev d;
         d.car = car; d.sim = sim; d.nSim = nSim; d.nBlue = nBlue; d.nCars = nCars; d.nTotal = nTotal; d.seed = seed;
-        d.arena = ArenaView{ rec, cellStart, angles, triRec, refBox, fineRec, fineAux, fineStart };
+        d.arena = ArenaView{ rec, cellStart, angles, triRec, refBox, refAng, fineRec, fineAux, fineStart };
         return d;
     }
     DoneRule rule() const { return DoneRule{ maxTicks, overtimeTicks, noTouchTicks }; }
@@ -495,7 +510,7 @@ int devAlloc(T** p, size_t count)
 
 void freeAll(carl_env* e)
 {
-    void* ptrs[] = { e->car, e->sim, e->rec, e->cellStart, e->angles, e->triRec, e->refBox, e->fineRec,
+    void* ptrs[] = { e->car, e->sim, e->rec, e->cellStart, e->angles, e->triRec, e->refBox, e->refAng, e->fineRec,
                      e->fineAux, e->fineStart, e->obs, e->tobs, e->state, e->tstate, e->rewards, e->dones,
                      e->overtime, e->tovertime, e->score, e->ticks, e->tscore, e->tticks, e->actions, e->cactions,
                      e->ws };
@@ -745,6 +760,7 @@ int carl_env_create(int nSim, int nBlue, int nOrange, int seed, int frameskip, i
     rc = rc ? rc : devAlloc(&e->angles, host.angles.size() / 3);
     rc = rc ? rc : devAlloc(&e->triRec, host.triRecords.size() / 4);
     rc = rc ? rc : devAlloc(&e->refBox, host.refBoxes.size() / 4);
+    rc = rc ? rc : devAlloc(&e->refAng, host.refAngles.size() / 4);
     rc = rc ? rc : devAlloc(&e->fineRec, host.fineRecords.size() / 4);
     rc = rc ? rc : devAlloc(&e->fineAux, host.fineAux.size() / 4);
     rc = rc ? rc : devAlloc(&e->fineStart, host.fineStart.size());
@@ -775,6 +791,8 @@ int carl_env_create(int nSim, int nBlue, int nOrange, int seed, int frameskip, i
         || hipMemcpy(e->triRec, host.triRecords.data(), host.triRecords.size() * sizeof(float), hipMemcpyHostToDevice)
                != hipSuccess
         || hipMemcpy(e->refBox, host.refBoxes.data(), host.refBoxes.size() * sizeof(float), hipMemcpyHostToDevice)
+               != hipSuccess
+        || hipMemcpy(e->refAng, host.refAngles.data(), host.refAngles.size() * sizeof(float), hipMemcpyHostToDevice)
                != hipSuccess
         || hipMemcpy(e->fineRec, host.fineRecords.data(), host.fineRecords.size() * sizeof(float),
                      hipMemcpyHostToDevice) != hipSuccess

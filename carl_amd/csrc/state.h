@@ -33,6 +33,7 @@ struct ArenaView {
     const float4* angles;    // signed edge angles per triangle (xyz)
     const float4* tri;       // 4 per triangle, by triangle index (same record layout)
     const float4* box;       // 4 per cell reference: contact-search screening data (arena.cpp)
+    const float4* refAng;    // per cell reference: the triangle's signed edge angles (xyz)
     const float4* fineRec;   // 4 per ball-grid reference (record layout)
     const float4* fineAux;   // per ball-grid reference: edge angles xyz, packed broadphase registration range
     const int* fineStart;    // kFineCells + 1 offsets into fineRec (in references)

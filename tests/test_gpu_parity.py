@@ -123,6 +123,27 @@ def test_dense_geometry_1v1_and_3v3(gpu):
         p.close()
 
 
+def test_balls_at_and_beyond_the_candidate_grid_edge(gpu):
+    """Balls inside the arena's broadphase box but outside the walls, and
+    beyond the box (where the sequential gather serves them), next to balls
+    on the floor, the walls and in the goals."""
+    rng = np.random.default_rng(15)
+    n = 64
+    p = Pair(n, 1, 1, seed=9, frameskip=2)
+    state = workloads.random_reset_state(rng, n, 2)
+    spots = np.array([[0.0, 0.0, 93.2], [4004.0, 100.0, 500.0], [4150.0, 0.0, 300.0], [4300.0, -200.0, 300.0],
+                      [0.0, 5300.0, 100.0], [0.0, 6100.0, 200.0], [100.0, 0.0, 2100.0], [-50.0, 30.0, 2250.0],
+                      [-4212.5, 0.0, 400.0], [0.0, -6031.0, 150.0]])
+    state["ball_position"] = np.ascontiguousarray(
+        spots[np.arange(n) % len(spots)] + rng.uniform(-2.0, 2.0, (n, 3)), dtype=np.float32)
+    p.apply_reset_state(state)
+    for step in range(20):
+        p.step_continuous(workloads.random_continuous_actions(rng, n, 2))
+        _assert_clean(p.state_mismatches(), f"state after step {step}")
+        _assert_clean(p.output_mismatches(), f"outputs after step {step}")
+    p.close()
+
+
 def test_2v2_masked_resets_every_step(gpu):
     """tick_skip 1 with 25% of arenas reset from random states each step (masked path)."""
     rng = np.random.default_rng(6)
