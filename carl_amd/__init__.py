@@ -17,7 +17,7 @@ try:
 except ImportError as exc:  # the product has no CPU fallback
     raise ImportError(
         "carl_amd requires its native HIP extension (libcarl_amd.so and _carl); "
-        "build it with `python -m carl_amd.build` "
+        "build it with `python carl_amd/build.py` "
         f"(PyTorch {_torch.__version__})"
     ) from exc
 

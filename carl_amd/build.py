@@ -1,7 +1,9 @@
 """Build the native parts of carl_amd in-tree.
 
-    python -m carl_amd.build          # engine + Python binding
-    python -m carl_amd.build --oracle # also the CPU oracle (test infrastructure)
+    python carl_amd/build.py          # engine + Python binding
+    python carl_amd/build.py --oracle # also the CPU oracle (test infrastructure)
+
+(Run by path: importing the carl_amd package needs the extension built here.)
 
 Outputs (next to this file):
   libcarl_amd.so   HIP engine for gfx950 + C-ABI (include/carl_amd.h)
