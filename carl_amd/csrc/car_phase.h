@@ -958,23 +958,29 @@ constexpr float kRotErr = 100.f * 0x1p-24f;    // rotated vertex error per unit 
 constexpr float kRotErr2 = 2.f * kRotErr;      // the same for an edge (two vertices)
 constexpr float kHalfLen = 80.f;               // |kHalf| rounded up
 
+// Cars searched per wave (owner lanes 0..kContactOwners-1); the other lanes
+// only take part in the cooperative item loop.  Sizing the per-owner LDS for
+// the owners alone keeps the block's LDS small enough that the kernel's
+// occupancy is set by its registers.
+constexpr int kContactOwners = 32;
+
 struct ContactLds {
     int excl[64];
-    int first[64];   // first cell reference of the owner's run
-    int satOn[64];   // owner takes part in the car-arena search (not demoed)
-    float rot[4][64];
-    float start[kWheels][3][64];
+    int first[kContactOwners];   // first cell reference of the owner's run
+    int satOn[kContactOwners];   // owner takes part in the car-arena search (not demoed)
+    float rot[4][kContactOwners];
+    float start[kWheels][3][kContactOwners];
     // screening, per owner: (cen, rayLo.x) (ax, rayLo.y) (ay, rayLo.z)
     // (az, rayHi.x) (rayHi.y, rayHi.z, screened, satOn); ax..az are the car's
     // box axes, ray* the box of the four ray segments
-    float4 scr[5][64];
-    float nearPos[kMaxManifold][3][64];
-    int nearN[64];
-    int satHits[64];
-    unsigned long long rayKey[kWheels][64];
-    unsigned long long bestKey[64];
-    float rayNrm[kWheels][3][64];   // surface normal of each wheel's nearest arena hit
-    float bestPt[10][64];           // manifold point of the deepest arena contact so far
+    float4 scr[5][kContactOwners];
+    float nearPos[kMaxManifold][3][kContactOwners];
+    int nearN[kContactOwners];
+    int satHits[kContactOwners];
+    unsigned long long rayKey[kWheels][kContactOwners];
+    unsigned long long bestKey[kContactOwners];
+    float rayNrm[kWheels][3][kContactOwners];   // surface normal of each wheel's nearest arena hit
+    float bestPt[10][kContactOwners];           // manifold point of the deepest arena contact so far
     // screened items in run order, entries owner << 24 | item
     int candQ[128];
     int candN;
@@ -1173,9 +1179,11 @@ DI void contactDrain(const Dev& d, ContactLds& L, int lane, bool last)
 }
 
 // Owner side, before the search: pose, rays and (with sat) the plane points
-// of the car-arena search into LDS.
+// of the car-arena search into LDS.  Lanes past the owners only reset the queue.
 DI void contactPrepare(ContactLds& L, int lane, bool sat, V3 cen, Q4 rot, int first, bool screen)
 {
+    if (lane == 0) L.candN = 0;
+    if (lane >= kContactOwners) return;
     const V3 dir = -rotate(rot, kZ);
     L.first[lane] = first;
     L.satOn[lane] = sat;
@@ -1209,7 +1217,6 @@ DI void contactPrepare(ContactLds& L, int lane, bool sat, V3 cen, Q4 rot, int fi
     }
     L.satHits[lane] = 0;
     L.bestKey[lane] = kNoKey;
-    if (lane == 0) L.candN = 0;
 }
 
 // Owner side, after the search: wheel hits (arena winner, then cars and the

@@ -1,16 +1,19 @@
 // engine.hip - kernels, host engine and C-ABI of the MI355X CARL step engine.
 //
-// Tick pipeline: one launch runs a whole frameskip window.  A workgroup owns
-// a tile of whole simulations (lanes = cars), so the reference's eleven
-// per-tick launches (src/RLEnvironment.cu:166-211) become phases separated by
-// workgroup barriers:
-//   A1  per car: broadphase + suspension raycast   (reads other cars' poses)
-//   A2  per car: controls, car-arena SAT/clip/manifold, suspension + solve
-//   B   per sim: episode tick, car-car pairs, ball arena + car-ball + goal
-//   C   per car: integrate + impulse cache / demo respawn; per sim: ball finish
-//   D   per sim: boost pads
-// State stays in the structure-of-arrays planes (L2 / MALL resident between
-// phases); no per-tick workspace buffers exist.
+// Tick pipeline: the reference's eleven per-tick launches plus a device scan
+// (src/RLEnvironment.cu:166-211) become five kernels per tick, in the
+// reference's stage order:
+//   contactKernel   per car: broadphase, suspension raycast and car-arena
+//                   contact search (wave-cooperative over the cell runs)
+//   carArenaKernel  per car: controls, suspension, manifold and solve
+//   carCarKernel    per sim: episode clock, car-car pairs
+//   ballKernel      per sim: ball-arena contacts, car-ball pairs, goals
+//   finishKernel    per car: integrate + impulse caches / demo respawn;
+//                   per sim: ball finish, then boost pads
+// The simulations are split into up to four partitions, each ticked on its
+// own stream.  State stays in the structure-of-arrays planes; the contact
+// kernel hands the car-arena kernel a small per-car workspace (wheel hits and
+// the deepest arena contact).
 #include <dlfcn.h>
 #include <hip/hip_runtime.h>
 
@@ -71,7 +74,7 @@ struct SimRange {
 // more waves: the work is latency-bound and 65536 1v1 simulations would
 // otherwise leave two waves per SIMD.
 constexpr int kContactBlock = 64;
-constexpr int kContactOwners = 32;
+static_assert(kContactOwners <= kContactBlock, "owners are lanes of the block");
 
 __global__ __launch_bounds__(kContactBlock) void contactKernel(Dev d, uint32_t* __restrict__ ws, int screen, SimRange range)
 {
@@ -320,9 +323,9 @@ __global__ __launch_bounds__(kContactBlock) void refreshKernel(Dev d, Selection 
 {
     __shared__ ContactLds L;
     const int lane = threadIdx.x;
-    const int src = blockIdx.x * kContactBlock + lane;
+    const int src = blockIdx.x * kContactOwners + lane;
     int car = -1;
-    if (src < sel.n * d.nCars) {
+    if (lane < kContactOwners && src < sel.n * d.nCars) {
         const int t = selectRow(sel, src / d.nCars, d.nSim);
         if (t >= 0) car = t * d.nCars + src % d.nCars;
     }
@@ -670,7 +673,7 @@ int setCarRows(carl_env* e, const float* pos, const float* rot, const float* vel
     setCarKernel<<<e->grid(n, 256), 256, 0, e->stream>>>(e->dev(), pos, rot, vel, ang, demoed, byteDemoed, boost,
                                                           internal, sel);
     HIP_TRY(hipGetLastError());
-    refreshKernel<<<e->grid(n, kContactBlock), kContactBlock, 0, e->stream>>>(e->dev(), sel, e->contactScreen);
+    refreshKernel<<<e->grid(n, kContactOwners), kContactBlock, 0, e->stream>>>(e->dev(), sel, e->contactScreen);
     HIP_TRY(hipGetLastError());
     return CARL_OK;
 }
