@@ -14,7 +14,7 @@ Prints one JSON line:
                  n_sim) / its average launch time, from HIP events the engine
                  records around every tick kernel on its own stream during
                  the timed steps, against 8 TB/s
-  tick_pipeline  the whole tick (five kernels) against the 1,488 B per 1v1
+  tick_pipeline  the whole tick (four kernels) against the 1,488 B per 1v1
                  sim-tick floor: persistent state read + written + actions
   cpu_baseline   the CPU model of the same physics (oracle/liboracle.so), one
                  1v1 arena per thread on this host's cores, direct controls
@@ -50,10 +50,10 @@ def kernel_bytes(kernel: str, n_cars: int) -> int:
                  workspace written; per sim: ball position (3 words)
       carArena   per car: workspace 21 + actions 7 + car state 54 words read,
                  car state 69 words written
-      carCar     per pair: both cars' demo flag, centre and rotation (16
-                 words); per sim: episode clock read + written (2 words)
-      ball       per sim: ball state 28 words read, 30 written; per car: demo
-                 flag, centre and last-hit tick (5 words)
+      ball       per pair: both cars' demo flag, centre and rotation (16
+                 words); per sim: episode clock read + written (2 words),
+                 ball state 28 words read, 30 written; per car: demo flag,
+                 centre and last-hit tick (5 words)
       finish     per car: 18 words read, 17 written; per sim: 34 pad
                  cooldowns read, ball velocity/spin/impulse 9 read + 9 written
     """
@@ -61,8 +61,7 @@ def kernel_bytes(kernel: str, n_cars: int) -> int:
     words = {
         "contactKernel": n_cars * (17 + 21) + 3,
         "carArenaKernel": n_cars * (21 + 7 + 54 + 69),
-        "carCarKernel": pairs * 16 + 2,
-        "ballKernel": 28 + 30 + n_cars * 5,
+        "ballKernel": pairs * 16 + 2 + 28 + 30 + n_cars * 5,
         "finishKernel": n_cars * (18 + 17) + 34 + 18,
     }[kernel]
     return 4 * words

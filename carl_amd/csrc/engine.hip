@@ -1,13 +1,13 @@
 // engine.hip - kernels, host engine and C-ABI of the MI355X CARL step engine.
 //
 // Tick pipeline: the reference's eleven per-tick launches plus a device scan
-// (src/RLEnvironment.cu:166-211) become five kernels per tick, in the
+// (src/RLEnvironment.cu:166-211) become four kernels per tick, in the
 // reference's stage order:
 //   contactKernel   per car: broadphase, suspension raycast and car-arena
 //                   contact search (wave-cooperative over the cell runs)
 //   carArenaKernel  per car: controls, suspension, manifold and solve
-//   carCarKernel    per sim: episode clock, car-car pairs
-//   ballKernel      per sim: ball-arena contacts, car-ball pairs, goals
+//   ballKernel      per sim: episode clock, car-car pairs, ball-arena
+//                   contacts, car-ball pairs, goals
 //   finishKernel    per car: integrate + impulse caches / demo respawn;
 //                   per sim: ball finish, then boost pads
 // The simulations are split into up to four partitions, each ticked on its
@@ -161,21 +161,23 @@ __global__ __launch_bounds__(kTickBlock, 2) void carArenaKernel(Dev d, const uin
     storeRegs(d, car, r);
 }
 
-// B1: episode clock and the car-car pairs of each simulation, (b, a) with b
-// the later car.
-__global__ __launch_bounds__(kTickBlock) void carCarKernel(Dev d, int tick, SimRange range)
+// Episode clock and the car-car pairs of one simulation, (b, a) with b the
+// later car (Kernels.cu:42-55, CarCar/Solve.cuh:63-151).
+DI void carCarSim(const Dev& d, int sim, int tick)
 {
-    const int sim = range.begin + blockIdx.x * kTickBlock + threadIdx.x;
-    if (sim >= range.end) return;
     d.sseti(CARL_SIM_EPISODE_TICKS, sim, d.si(CARL_SIM_EPISODE_TICKS, sim) + 1);
     const int base = sim * d.nCars;
     for (int a = 0; a < d.nCars - 1; a++)
         for (int b = a + 1; b < d.nCars; b++) carCarPair(d, base + b, base + a, tick);
 }
 
-// B2: ball-arena contacts, car-ball pairs and goal detection.  One wave per
-// block; the arena contacts of its kBallOwners balls are gathered by all 64
-// lanes cooperatively.
+// B: per simulation the episode clock and the car-car pairs, then ball-arena
+// contacts, car-ball pairs and goal detection (the reference's
+// carCarBallSolveKernel, Kernels.cu:162-172).  One wave per block; the arena
+// contacts of its kBallOwners balls are gathered by all 64 lanes
+// cooperatively.  The car-car solve of a colliding pair is a long serial
+// chain on one lane: inside this kernel it delays only its own wave, where a
+// kernel of its own would end only when that chain ends.
 constexpr int kBallBlock = 64;
 constexpr int kBallOwners = 32;
 
@@ -185,6 +187,7 @@ __global__ __launch_bounds__(kBallBlock) void ballKernel(Dev d, int tick, SimRan
     const int lane = threadIdx.x;
     const int sim = range.begin + blockIdx.x * kBallOwners + lane;
     const bool ok = lane < kBallOwners && sim < range.end;
+    if (ok) carCarSim(d, sim, tick);
     const bool awake = ok && !ballSleeping(d, sim);
     const V3 center = ok ? d.sv(CARL_SIM_BALL_POS, sim) : kZero;
     int items = 0, first = 0, cell = 0;
@@ -581,8 +584,6 @@ int launchTicks(carl_env* e, int kind, const void* actions, int n)
             contactKernel<<<e->grid(cars, kContactOwners), kContactBlock, 0, st>>>(d, e->ws, e->contactScreen, r);
             if (timed) CARL_MARK(CARL_KERNEL_CAR_ARENA);
             carArenaKernel<<<e->grid(cars, kTickBlock), kTickBlock, 0, st>>>(d, e->ws, kind, actions, tick, r);
-            if (timed) CARL_MARK(CARL_KERNEL_CAR_CAR);
-            carCarKernel<<<e->grid(sims, kTickBlock), kTickBlock, 0, st>>>(d, tick, r);
             if (timed) CARL_MARK(CARL_KERNEL_BALL);
             ballKernel<<<e->grid(sims, kBallOwners), kBallBlock, 0, st>>>(d, tick, r);
             if (timed) CARL_MARK(CARL_KERNEL_FINISH);
@@ -1064,8 +1065,7 @@ int carl_env_tick_timing(carl_env* e, double* kernelMs, int* launches)
 
 const char* carl_tick_kernel_name(int kernel)
 {
-    static const char* names[CARL_TICK_KERNELS] = { "contactKernel", "carArenaKernel", "carCarKernel", "ballKernel",
-                                                    "finishKernel" };
+    static const char* names[CARL_TICK_KERNELS] = { "contactKernel", "carArenaKernel", "ballKernel", "finishKernel" };
     return kernel >= 0 && kernel < CARL_TICK_KERNELS ? names[kernel] : "";
 }
 

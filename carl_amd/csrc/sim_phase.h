@@ -218,7 +218,10 @@ DI void pairPush(Body& A, Body& B, const PairRow& r, float imp, bool split)
     }
 }
 
-// 2-body sequential impulses with split penetration recovery (CarCar/Solver.cuh:187-244)
+// 2-body sequential impulses with split penetration recovery (CarCar/Solver.cuh:187-244).
+// The friction rows are built after the split-impulse loop: their inputs (the
+// pre-solve velocities, poses and contact normals) are not changed by it, so
+// the rows are the same, and they need no registers during that loop.
 DI void solvePair(Body& A, Body& B, const PairContact* cts, int count)
 {
     PairRow nr[kMaxManifold], fr[kMaxManifold];
@@ -234,15 +237,6 @@ DI void solvePair(Body& A, Body& B, const PairContact* cts, int count)
         n.rhs = (bounce - rv) * n.jacInv;
         n.rhsPen = pen * kContactErp / kDt * n.jacInv;
         nr[i] = n;
-        const V3 rel = (A.vel + cross(A.ang, relA)) - (B.vel + cross(B.ang, relB));
-        const float nv = dot(cts[i].normal, rel);
-        V3 tan = rel - cts[i].normal * nv;
-        const float tl = lensq(tan);
-        const float thr = fmax_(kFltEps, nv * nv * 1e-8f);
-        tan = tl > thr ? tan * rsqrt_(tl) : fallbackTangent(cts[i].normal);
-        PairRow t = pairRow(A, B, tan, relA, relB);
-        t.rhs = -pairVel(t, A.vel, A.ang, B.vel, B.ang) * t.jacInv;
-        fr[i] = t;
     }
     for (int it = 0; it < kSolverIters; it++) {
 #pragma unroll
@@ -253,6 +247,21 @@ DI void solvePair(Body& A, Body& B, const PairContact* cts, int count)
                                        r.appliedPush);
             pairPush(A, B, r, imp, true);
         }
+    }
+#pragma unroll
+    for (int i = 0; i < kMaxManifold; i++) {
+        if (i >= count) break;
+        const V3 relA = (A.cen - A.pos) + rotate(A.rot, cts[i].posA);
+        const V3 relB = (B.cen - B.pos) + rotate(B.rot, cts[i].posB);
+        const V3 rel = (A.vel + cross(A.ang, relA)) - (B.vel + cross(B.ang, relB));
+        const float nv = dot(cts[i].normal, rel);
+        V3 tan = rel - cts[i].normal * nv;
+        const float tl = lensq(tan);
+        const float thr = fmax_(kFltEps, nv * nv * 1e-8f);
+        tan = tl > thr ? tan * rsqrt_(tl) : fallbackTangent(cts[i].normal);
+        PairRow t = pairRow(A, B, tan, relA, relB);
+        t.rhs = -pairVel(t, A.vel, A.ang, B.vel, B.ang) * t.jacInv;
+        fr[i] = t;
     }
     for (int it = 0; it < kSolverIters; it++) {
 #pragma unroll

@@ -288,16 +288,15 @@ int carl_env_import_state(carl_env* env, const uint32_t* car_state,
                           const uint32_t* sim_state, int tick_count);
 
 /* ---- tick-kernel timing (no reference counterpart) -------------------------
- * One physics tick is five kernels on the environment stream, in this order
+ * One physics tick is four kernels on the environment stream, in this order
  * (the reference's eleven per-tick launches, src/RLEnvironment.cu:166-211,
  * grouped by the data they own). */
 enum {
     CARL_KERNEL_CONTACT = 0,    /* broadphase, wheel rays, car-arena contact search */
     CARL_KERNEL_CAR_ARENA = 1,  /* controls, suspension, car-arena solve */
-    CARL_KERNEL_CAR_CAR = 2,    /* episode clock, car-car pairs */
-    CARL_KERNEL_BALL = 3,       /* ball-arena, car-ball, goal */
-    CARL_KERNEL_FINISH = 4,     /* integration, impulse caches, boost pads */
-    CARL_TICK_KERNELS = 5
+    CARL_KERNEL_BALL = 2,       /* episode clock, car-car pairs, ball-arena, car-ball, goal */
+    CARL_KERNEL_FINISH = 3,     /* integration, impulse caches, boost pads */
+    CARL_TICK_KERNELS = 4
 };
 
 /* With timing enabled, HIP events recorded on the environment stream bracket
