@@ -148,11 +148,11 @@ constexpr int kObsPerCar = 21;
 constexpr int kStatePerCar = 22;
 constexpr int kInternalFields = 19;
 
-HDI int observationDim(int nCars, bool prev)
+HDI constexpr int observationDim(int nCars, bool prev)
 {
     return 9 + nCars * kObsPerCar + 2 * kPads + 6 + (nCars - 1) * 6 + 6 + 2 + 5 + (prev ? 8 : 0);
 }
-HDI int stateDim(int nCars) { return 9 + nCars * kStatePerCar + kPads; }
+HDI constexpr int stateDim(int nCars) { return 9 + nCars * kStatePerCar + kPads; }
 
 // wheel geometry
 HDI V3 wheelAnchor(int w)

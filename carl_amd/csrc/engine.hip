@@ -281,20 +281,72 @@ __global__ void matchKernel(Dev d, int* score, int* ticks, bool* overtime, const
     overtime[s] = d.si(CARL_SIM_OVERTIME, s) != 0;
 }
 
-__global__ void stateKernel(Dev d, float* out, int stateDimV, int touchWindow, int tickCount, const bool* mask)
+// Row-major outputs (observations, canonical states) are written through
+// LDS: each lane builds one row there, then the wave stores the block's rows
+// as one contiguous run, so each store instruction covers consecutive words.
+// A lane storing its own row would touch a different line per lane and per
+// store, and lines evicted half-written cost extra HBM writes.  Rows are at
+// least kPackBlock words long (the shortest is the 1-car state, 65), so the
+// row/column position of a lane advances by at most one row per round.
+// A block stages at most kPackLdsBytes of rows (16 rows of a 1v1
+// observation): the row-building phase is latency-bound, and small blocks
+// keep more of them resident per CU (measured 40 KB -> 10 KB: +2% per env step).
+constexpr int kPackBlock = 64;
+constexpr int kPackLdsBytes = 10 * 1024;
+
+// odd row stride: the lanes' row writes fall in distinct LDS banks
+HDI int packStride(int rowLen) { return rowLen | 1; }
+HDI int packRowsPerBlock(int rowLen)
 {
-    const int s = blockIdx.x * blockDim.x + threadIdx.x;
-    if (s >= d.nSim || (mask && !mask[s])) return;
-    packStateRow(d, s, touchWindow, tickCount, out + (size_t)s * stateDimV);
+    int rows = kPackBlock;
+    while (rows > 8 && rows * packStride(rowLen) * 4 > kPackLdsBytes) rows /= 2;
+    return rows;
 }
 
-__global__ void obsKernel(Dev d, float* out, int obsDimV, const bool* mask, int invert, int normalizeObs, int prev)
+static_assert(stateDim(1) > kPackBlock && observationDim(1, false) > kPackBlock,
+              "packRows steps a lane by less than one row per round");
+
+// Rows [r0, r0 + rowsPerBlock) of out (nRows rows of rowLen floats); row r is
+// built by row(r, dst) when simMask is null or simMask[r / rowsPerSim] is set,
+// and only those rows are stored.
+template <typename Row>
+DI void packRows(float* out, int rowLen, int nRows, int rowsPerBlock, const bool* simMask, int rowsPerSim, Row&& row)
 {
-    const int a = blockIdx.x * blockDim.x + threadIdx.x;
-    if (a >= d.nTotal) return;
-    const int s = a / d.nCars;
-    if (mask && !mask[s]) return;
-    packObservation(d, s, a % d.nCars, invert != 0, normalizeObs != 0, prev != 0, out + (size_t)a * obsDimV);
+    extern __shared__ float packLds[];
+    __shared__ int on[kPackBlock];
+    const int lane = threadIdx.x;
+    const int stride = packStride(rowLen);
+    const int r0 = blockIdx.x * rowsPerBlock;
+    const int r = r0 + lane;
+    const bool mine = lane < rowsPerBlock && r < nRows && (!simMask || simMask[r / rowsPerSim]);
+    if (!__any(mine)) return;   // whole wave: no row of this block is packed
+    if (mine) row(r, packLds + lane * stride);
+    on[lane] = mine;
+    __syncthreads();
+    const int rows = min(rowsPerBlock, nRows - r0);
+    const int total = rows * rowLen;
+    float* dst = out + (size_t)r0 * rowLen;
+    int rr = 0, c = lane;
+    for (int e = lane; e < total; e += kPackBlock) {
+        if (on[rr]) dst[e] = packLds[rr * stride + c];
+        c += kPackBlock;
+        if (c >= rowLen) { c -= rowLen; rr++; }
+    }
+}
+
+__global__ __launch_bounds__(kPackBlock) void stateKernel(Dev d, float* out, int stateDimV, int rowsPerBlock,
+                                                         int touchWindow, int tickCount, const bool* mask)
+{
+    packRows(out, stateDimV, d.nSim, rowsPerBlock, mask, 1,
+             [&](int s, float* o) { packStateRow(d, s, touchWindow, tickCount, o); });
+}
+
+__global__ __launch_bounds__(kPackBlock) void obsKernel(Dev d, float* out, int obsDimV, int rowsPerBlock,
+                                                       const bool* mask, int invert, int normalizeObs, int prev)
+{
+    packRows(out, obsDimV, d.nTotal, rowsPerBlock, mask, d.nCars, [&](int a, float* o) {
+        packObservation(d, a / d.nCars, a % d.nCars, invert != 0, normalizeObs != 0, prev != 0, o);
+    });
 }
 
 __global__ void setBallKernel(Dev d, const float* pos, const float* vel, const float* ang, Selection sel)
@@ -603,16 +655,20 @@ int launchTicks(carl_env* e, int kind, const void* actions, int n)
 
 int packObs(carl_env* e, float* out, const bool* mask)
 {
-    obsKernel<<<e->grid(e->nTotal, 128), 128, 0, e->stream>>>(e->dev(), out, e->obsDim, mask, e->invert, e->normalize,
-                                                              e->prevControls);
+    const int rows = packRowsPerBlock(e->obsDim);
+    const size_t lds = (size_t)rows * packStride(e->obsDim) * sizeof(float);
+    obsKernel<<<e->grid(e->nTotal, rows), kPackBlock, lds, e->stream>>>(e->dev(), out, e->obsDim, rows, mask, e->invert,
+                                                                       e->normalize, e->prevControls);
     HIP_TRY(hipGetLastError());
     return CARL_OK;
 }
 
 int packState(carl_env* e, float* out, int touchWindow, const bool* mask)
 {
-    stateKernel<<<e->grid(e->nSim, 64), 64, 0, e->stream>>>(e->dev(), out, e->stateDim, touchWindow, e->tickCount,
-                                                            mask);
+    const int rows = packRowsPerBlock(e->stateDim);
+    const size_t lds = (size_t)rows * packStride(e->stateDim) * sizeof(float);
+    stateKernel<<<e->grid(e->nSim, rows), kPackBlock, lds, e->stream>>>(e->dev(), out, e->stateDim, rows, touchWindow,
+                                                                       e->tickCount, mask);
     HIP_TRY(hipGetLastError());
     return CARL_OK;
 }
