@@ -64,6 +64,10 @@ void oracle_cell_of(float x, float y, float z, int* cell3);
 void oracle_broadphase(OEnv* e, int32_t* cell, int32_t* count);
 /* suspension raycast of every car: dist [n,4], normal [n,4,3], source [n,4] */
 void oracle_raycast(OEnv* e, float* dist, float* normal, int32_t* source);
+/* ball-arena contacts for a ball centred at `center` (at most 68): triangle,
+ * point [3], normal [3], depth, reduction offset [3]; returns the count */
+int oracle_ball_contacts(OEnv* e, const float* center, int32_t* tri, float* point, float* normal,
+                         float* depth, float* reduction);
 
 /* known-answer probes (tests/physics_regressions.cu, tests/turtle_recovery.cu) */
 int oracle_ball_hit_prev_tick(int hit_tick, int tick);

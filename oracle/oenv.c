@@ -765,6 +765,12 @@ void oracle_raycast(OEnv* e, float* dist, float* normal, int32_t* source)
     }
 }
 
+int oracle_ball_contacts(OEnv* e, const float* center, int32_t* tri, float* point, float* normal, float* depth,
+                         float* reduction)
+{
+    return ophys_probe_ball_contacts(&e->w, center, tri, point, normal, depth, reduction);
+}
+
 /* ------------------------------------------------------------------ probes */
 
 int oracle_ball_hit_prev_tick(int h, int t) { return ophys_ball_hit_prev_tick(h, t); }

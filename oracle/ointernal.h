@@ -315,6 +315,8 @@ void ophys_probe_box_box_sat(const float* cenA, const float* rotA, const float* 
                              int* overlap, int* axisIdx, float* depth);
 V3 ophys_pad_pos(int pad);
 int ophys_ball_hit_prev_tick(int hitTick, int tick);
+int ophys_probe_ball_contacts(const OWorld* w, const float* center, int* tri, float* point, float* normal,
+                              float* depth, float* reduction);
 
 /* unit probes of reference behaviours (used by the known-answer tests) */
 void ophys_probe_dodge(float pitch, float yaw, float roll, int* hasFlipped,

@@ -21,11 +21,15 @@
  * tick agree bit for bit between the two.
  *
  * Pinned by the reference's own known-answer tests, its tables, closed forms,
- * linear-programming SAT checks and brute-force mesh searches (tests/).
+ * linear-programming SAT checks, brute-force mesh searches and physics laws
+ * (momentum, restitution, Coulomb friction, spring equilibrium, rolling) on
+ * isolated contacts (tests/).
  * PARITY UNPINNED (no independent check; engine and oracle agree with each
- * other only): suspension forces beyond the at-rest equilibrium, the PGS
- * solver internals, car-car bump/demo impulses, the car-ball extra impulse,
- * the ball contact reduction and edge adjustment.
+ * other only): the ground drive and wheel friction curves, the jump impulse
+ * timeline, flip impulses and torques, air-control torques and damping,
+ * auto-roll; among several car-mesh clip contacts, which one is kept and its
+ * car-side point; the edge-edge contacts of car-mesh and car-car SAT and the
+ * car-side internal-edge adjustment.
  */
 #ifndef CARL_ORACLE_MATH_H
 #define CARL_ORACLE_MATH_H

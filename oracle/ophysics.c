@@ -1920,6 +1920,26 @@ static void solve_ball_contacts(OBallBody* b, const OBallContact* cs, int count,
     if (as > K_BALL_MAX_ANG * K_BALL_MAX_ANG) b->ang = vscale(b->ang, K_BALL_MAX_ANG * o_rsqrt(as));
 }
 
+/* Test probe: the ball-arena contacts gathered for a ball centred at
+ * `center`, in slot order: triangle, contact point, normal (after the
+ * internal-edge adjustment), depth, and the pre-adjustment offset from the
+ * centre used by the reduction.  Returns the count. */
+int ophys_probe_ball_contacts(const OWorld* w, const float* center, int* tri, float* point, float* normal,
+                              float* depth, float* reduction)
+{
+    OBallContact cs[MAX_BALL_CONTACTS];
+    const int n = gather_ball_contacts(w->arena, v3(center[0], center[1], center[2]), cs);
+    for (int i = 0; i < n; i++) {
+        tri[i] = cs[i].tri;
+        point[3 * i] = cs[i].point.x; point[3 * i + 1] = cs[i].point.y; point[3 * i + 2] = cs[i].point.z;
+        normal[3 * i] = cs[i].normal.x; normal[3 * i + 1] = cs[i].normal.y; normal[3 * i + 2] = cs[i].normal.z;
+        depth[i] = cs[i].depth;
+        reduction[3 * i] = cs[i].reductionPos.x; reduction[3 * i + 1] = cs[i].reductionPos.y;
+        reduction[3 * i + 2] = cs[i].reductionPos.z;
+    }
+    return n;
+}
+
 int ophys_ball_hit_prev_tick(int hitTick, int tick) { return hitTick >= 0 && tick > 0 && hitTick == tick - 1; }
 
 /* ------------------------------------------------------------- ball vs car */

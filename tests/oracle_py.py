@@ -49,6 +49,7 @@ def lib():
         L.oracle_cell_of.argtypes = [C.c_float, C.c_float, C.c_float, ip]
         L.oracle_broadphase.argtypes = [vp, ip, ip]
         L.oracle_raycast.argtypes = [vp, fp, fp, ip]
+        L.oracle_ball_contacts.argtypes = [vp, fp, ip, fp, fp, fp, fp]
         L.oracle_ball_hit_prev_tick.argtypes = [C.c_int, C.c_int]
         L.oracle_probe_ball_floor_split.restype = C.c_float
         L.oracle_probe_ball_floor_split.argtypes = [C.c_float, C.c_float, C.c_int]
@@ -234,6 +235,19 @@ class OracleEnv:
                                 ang.ctypes.data_as(fpp), prefix.ctypes.data_as(ipp),
                                 cell_tris.ctypes.data_as(ipp))
         return verts, tris, ang, prefix, cell_tris[:nr.value]
+
+    def ball_contacts(self, center):
+        """Ball-arena contacts gathered for a ball centred at `center`, in
+        slot order: (triangles, points, normals, depths, reduction offsets)."""
+        tri = np.zeros(68, np.int32)
+        pt, nrm, red = np.zeros((68, 3), np.float32), np.zeros((68, 3), np.float32), np.zeros((68, 3), np.float32)
+        dep = np.zeros(68, np.float32)
+        c = np.ascontiguousarray(center, np.float32)
+        fp = C.POINTER(C.c_float)
+        n = lib().oracle_ball_contacts(self.h, c.ctypes.data_as(fp), tri.ctypes.data_as(C.POINTER(C.c_int)),
+                                       pt.ctypes.data_as(fp), nrm.ctypes.data_as(fp), dep.ctypes.data_as(fp),
+                                       red.ctypes.data_as(fp))
+        return tri[:n], pt[:n], nrm[:n], dep[:n], red[:n]
 
     def broadphase(self):
         n = self.n_sim * self.n_cars
