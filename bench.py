@@ -42,10 +42,12 @@ def tick_bytes(n_cars: int) -> int:
     return 2 * (n_cars * BYTES_PER_CAR + BYTES_PER_SIM) + n_cars * ACTION_BYTES
 
 
-def kernel_bytes(kernel: str, n_cars: int) -> int:
+def kernel_bytes(kernel: str, n_cars: int, ticks: int) -> int:
     """Algorithmic HBM bytes per simulation of one launch of a tick kernel, on
     the common path (no demolition, no car-car contact, ball awake): the state
     words the kernel must read and write once each.
+      tickWindow every tick of the step (`ticks`) in one launch: the tick
+                 floor (persistent state read + written, actions) per tick
       contact    per car: pose/velocity/demo flag 17 words read, 21-word
                  workspace written; per sim: ball position (3 words)
       carArena   per car: workspace 21 + actions 7 + car state 54 words read,
@@ -57,6 +59,8 @@ def kernel_bytes(kernel: str, n_cars: int) -> int:
       finish     per car: 18 words read, 17 written; per sim: 34 pad
                  cooldowns read, ball velocity/spin/impulse 9 read + 9 written
     """
+    if kernel == "tickWindowKernel":
+        return tick_bytes(n_cars) * ticks
     pairs = n_cars * (n_cars - 1) // 2
     words = {
         "contactKernel": n_cars * (17 + 21) + 3,
@@ -117,6 +121,9 @@ def main() -> None:
                     help="CPU-baseline ticks per host thread (0 skips it)")
     ap.add_argument("--tick-streams", type=int, default=0,
                     help="partitions of the simulations ticked on separate streams (0: engine default)")
+    ap.add_argument("--tick-window", type=int, default=-1,
+                    help="simulations per workgroup of the tick-window kernel, 0 for phase kernels "
+                         "(-1: engine default)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (HBM counter calibration) and exit")
     args = ap.parse_args()
@@ -149,6 +156,8 @@ def main() -> None:
     stream = torch.cuda.ExternalStream(env.stream, device=dev)
     if args.tick_streams:
         env.tick_streams = args.tick_streams
+    if args.tick_window >= 0:
+        env.tick_window = args.tick_window
 
     odd = np.arange(1, n_sim, 2)
     reset = workloads.random_reset_state(rng, len(odd), n_cars)
@@ -189,7 +198,7 @@ def main() -> None:
     # partition 0, which holds n_sim // tick_streams of them
     parts = min(env.tick_streams, n_sim)
     launch_sims = n_sim // parts
-    launch_bytes = kernel_bytes(kernel, n_cars) * launch_sims
+    launch_bytes = kernel_bytes(kernel, n_cars, args.tick_skip) * launch_sims
     achieved = launch_bytes / (launch_ms * 1e-3) / 1e9
     tick_ms = sum(ms for ms, _ in timing.values())
 
@@ -216,6 +225,7 @@ def main() -> None:
             "tick_skip": args.tick_skip,
             "parallelism": "single GPU",
             "tick_streams": parts,
+            "tick_window": env.tick_window,
         },
         "roofline": {
             "bound": "hbm",

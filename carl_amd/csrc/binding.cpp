@@ -489,7 +489,7 @@ public:
         check(carl_env_tick_timing(env_, ms, launches));
         py::dict out;
         for (int k = 0; k < CARL_TICK_KERNELS; k++)
-            out[py::str(carl_tick_kernel_name(k))] = py::make_tuple(ms[k], launches[k]);
+            if (launches[k] > 0) out[py::str(carl_tick_kernel_name(k))] = py::make_tuple(ms[k], launches[k]);
         return out;
     }
 };
@@ -626,6 +626,8 @@ PYBIND11_MODULE(_carl, m)
                       [](Env& e, int v) { e.setParam(CARL_PARAM_TICK_STREAMS, v); })
         .def_property("contact_screen", [](Env& e) { return e.param(CARL_PARAM_CONTACT_SCREEN); },
                       [](Env& e, int v) { e.setParam(CARL_PARAM_CONTACT_SCREEN, v); })
+        .def_property("tick_window", [](Env& e) { return e.param(CARL_PARAM_TICK_WINDOW); },
+                      [](Env& e, int v) { e.setParam(CARL_PARAM_TICK_WINDOW, v); })
         .def_property_readonly("obs_dim", [](Env& e) { return e.param(CARL_PARAM_OBS_DIM); })
         .def_property_readonly("act_dim", [](Env& e) { return e.param(CARL_PARAM_ACT_DIM); })
         .def_property_readonly("action_nvec", &Env::actionNvec)

@@ -76,12 +76,13 @@ struct SimRange {
 constexpr int kContactBlock = 64;
 static_assert(kContactOwners <= kContactBlock, "owners are lanes of the block");
 
-__global__ __launch_bounds__(kContactBlock) void contactKernel(Dev d, uint32_t* __restrict__ ws, int screen, SimRange range)
+// The contact search of cars [car0, car0 + kContactOwners) (those below
+// carEnd) by one wave; L is that wave's own LDS.  Every lane of the wave calls
+// it; it synchronises the wave only.
+DI void contactGroup(const Dev& d, uint32_t* __restrict__ ws, int screen, int car0, int carEnd, ContactLds& L, int lane)
 {
-    __shared__ ContactLds L;
-    const int lane = threadIdx.x;
-    const int car = range.begin * d.nCars + blockIdx.x * kContactOwners + lane;
-    const bool ok = lane < kContactOwners && car < range.end * d.nCars;
+    const int car = car0 + lane;
+    const bool ok = lane < kContactOwners && car < carEnd;
     V3 cen = kZero;
     Q4 rot{ 0.f, 0.f, 0.f, 1.f };
     Broad bp{ 0, 0 };
@@ -93,12 +94,12 @@ __global__ __launch_bounds__(kContactBlock) void contactKernel(Dev d, uint32_t* 
         demoed = d.ci(CARL_CAR_DEMOED, car) != 0;
     }
     contactPrepare(L, lane, ok && !demoed, cen, rot, bp.start, screen != 0);
-    __syncthreads();
+    waveSync();
     waveItemsPipelined(
         bp.count, L.excl, [&](int o, int q, bool valid) { return contactFetch(d, L, o, q, valid); },
         [&](const RefBox& b, int o, int q, int) { contactScreen(L, b, o, q, lane); },
         [&](bool last) { contactDrain(d, L, lane, last); });
-    __syncthreads();
+    waveSync();
     if (!ok) return;
     Wheels w;
     const int best = contactFinish(d, L, lane, car, car / d.nCars, cen, rot, w);
@@ -118,14 +119,18 @@ __global__ __launch_bounds__(kContactBlock) void contactKernel(Dev d, uint32_t* 
     }
 }
 
+__global__ __launch_bounds__(kContactBlock) void contactKernel(Dev d, uint32_t* __restrict__ ws, int screen, SimRange range)
+{
+    __shared__ ContactLds L;
+    contactGroup(d, ws, screen, range.begin * d.nCars + blockIdx.x * kContactOwners, range.end * d.nCars, L,
+                 threadIdx.x);
+}
+
 // A2: controls, car-arena contacts, suspension and the contact solve.
 // two waves per SIMD keep all of its waves resident at 65536 1v1 simulations
-__global__ __launch_bounds__(kTickBlock, 2) void carArenaKernel(Dev d, const uint32_t* __restrict__ ws, int kind,
-                                                             const void* __restrict__ actions, int tick,
-                                                             SimRange range)
+DI void carArenaCar(const Dev& d, const uint32_t* __restrict__ ws, int kind, const void* __restrict__ actions,
+                    int tick, int car)
 {
-    const int car = range.begin * d.nCars + blockIdx.x * kTickBlock + threadIdx.x;
-    if (car >= range.end * d.nCars) return;
     const size_t n = d.nTotal;
     Wheels w;
 #pragma unroll
@@ -161,6 +166,14 @@ __global__ __launch_bounds__(kTickBlock, 2) void carArenaKernel(Dev d, const uin
     storeRegs(d, car, r);
 }
 
+__global__ __launch_bounds__(kTickBlock, 2) void carArenaKernel(Dev d, const uint32_t* __restrict__ ws, int kind,
+                                                             const void* __restrict__ actions, int tick,
+                                                             SimRange range)
+{
+    const int car = range.begin * d.nCars + blockIdx.x * kTickBlock + threadIdx.x;
+    if (car < range.end * d.nCars) carArenaCar(d, ws, kind, actions, tick, car);
+}
+
 // Episode clock and the car-car pairs of one simulation, (b, a) with b the
 // later car (Kernels.cu:42-55, CarCar/Solve.cuh:63-151).
 DI void carCarSim(const Dev& d, int sim, int tick)
@@ -181,12 +194,13 @@ DI void carCarSim(const Dev& d, int sim, int tick)
 constexpr int kBallBlock = 64;
 constexpr int kBallOwners = 32;
 
-__global__ __launch_bounds__(kBallBlock) void ballKernel(Dev d, int tick, SimRange range)
+// Simulations [sim0, sim0 + kBallOwners) (those below simEnd) by one wave; L
+// is that wave's own LDS.  Every lane of the wave calls it; it synchronises
+// the wave only.
+DI void ballGroup(const Dev& d, int tick, int sim0, int simEnd, BallLds& L, int lane)
 {
-    __shared__ BallLds L;
-    const int lane = threadIdx.x;
-    const int sim = range.begin + blockIdx.x * kBallOwners + lane;
-    const bool ok = lane < kBallOwners && sim < range.end;
+    const int sim = sim0 + lane;
+    const bool ok = lane < kBallOwners && sim < simEnd;
     if (ok) carCarSim(d, sim, tick);
     const bool awake = ok && !ballSleeping(d, sim);
     const V3 center = ok ? d.sv(CARL_SIM_BALL_POS, sim) : kZero;
@@ -201,7 +215,7 @@ __global__ __launch_bounds__(kBallBlock) void ballKernel(Dev d, int tick, SimRan
         }
     }
     ballPrepare(L, lane, center, first);
-    __syncthreads();
+    waveSync();
     BallContact cs[4];
 #pragma unroll
     for (int k = 0; k < 4; k++) cs[k] = BallContact{ kZero, kZero, kZero, 0.f, kZero };
@@ -231,6 +245,12 @@ __global__ __launch_bounds__(kBallBlock) void ballKernel(Dev d, int tick, SimRan
     ballTick(d, sim, tick, cs, count);
 }
 
+__global__ __launch_bounds__(kBallBlock) void ballKernel(Dev d, int tick, SimRange range)
+{
+    __shared__ BallLds L;
+    ballGroup(d, tick, range.begin + blockIdx.x * kBallOwners, range.end, L, threadIdx.x);
+}
+
 // C + D: integration and impulse caches of every car and ball, then the
 // boost pads of each simulation once all of its cars have moved.  A block
 // owns whole simulations (simsPerBlock * nCars car lanes).
@@ -246,6 +266,48 @@ __global__ __launch_bounds__(kTickBlock) void finishKernel(Dev d, int simsPerBlo
     if (simOk) finishBall(d, laneSim);
     __syncthreads();
     if (simOk) boostPads(d, laneSim);
+}
+
+// The whole tick window in one launch: a block owns simulations
+// [begin + blockIdx.x * simsPerBlock, +simsPerBlock) and runs every phase of
+// every tick on them, with block barriers between the phases.  Simulations
+// share nothing but the read-only arena, so no other block is ever waited
+// for: a slow wave holds up its own block, not a grid-wide kernel boundary.
+constexpr int kWindowBlock = 256;
+constexpr int kWindowWaves = kWindowBlock / 64;
+constexpr int kDefaultWindowSims = 128;
+
+union WindowLds {
+    ContactLds contact[kWindowWaves];
+    BallLds ball[kWindowWaves];
+};
+
+__global__ __launch_bounds__(kWindowBlock, 2) void tickWindowKernel(Dev d, uint32_t* __restrict__ ws, int screen,
+                                                                 int kind, const void* __restrict__ actions,
+                                                                 int tick0, int ticks, int simsPerBlock,
+                                                                 SimRange range)
+{
+    __shared__ WindowLds L;
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int sim0 = range.begin + blockIdx.x * simsPerBlock;
+    const int simEnd = min(sim0 + simsPerBlock, range.end);
+    const int car0 = sim0 * d.nCars, carEnd = simEnd * d.nCars;
+    for (int k = 0; k < ticks; k++) {
+        const int tick = tick0 + k;
+        for (int g = car0 + wave * kContactOwners; g < carEnd; g += kWindowWaves * kContactOwners)
+            contactGroup(d, ws, screen, g, carEnd, L.contact[wave], lane);
+        __syncthreads();
+        for (int c = car0 + t; c < carEnd; c += kWindowBlock) carArenaCar(d, ws, kind, actions, tick, c);
+        __syncthreads();
+        for (int g = sim0 + wave * kBallOwners; g < simEnd; g += kWindowWaves * kBallOwners)
+            ballGroup(d, tick, g, simEnd, L.ball[wave], lane);
+        __syncthreads();
+        for (int c = car0 + t; c < carEnd; c += kWindowBlock) finishCar(d, c);
+        for (int s = sim0 + t; s < simEnd; s += kWindowBlock) finishBall(d, s);
+        __syncthreads();
+        for (int s = sim0 + t; s < simEnd; s += kWindowBlock) boostPads(d, s);
+        __syncthreads();
+    }
 }
 
 __global__ void resetKernel(Dev d, int nOrange)
@@ -535,15 +597,17 @@ struct carl_env {
     int32_t* actions = nullptr;
     float* cactions = nullptr;
     uint32_t* ws = nullptr;  // per-tick car workspace (kWsPlanes planes)
-    int tickStreams = kMaxTickStreams;   // partitions of the tick, one stream each
+    int tickStreams = 1;                 // partitions of the tick, one stream each
     int contactScreen = 1;               // screen (car, triangle) pairs in the contact search
     hipStream_t aux[kMaxTickStreams - 1] = {};
     hipEvent_t fork = nullptr, join[kMaxTickStreams - 1] = {};
+    int windowSims = kDefaultWindowSims;  // simulations per block of the tick-window kernel (0: phase kernels)
     bool timing = false;
-    // timing markers: per timed tick, one event before each tick kernel and
-    // one after the last (CARL_TICK_KERNELS + 1); reusable pool
-    size_t timedTicks = 0;
+    // timing: per timed launch a start and an end event (reusable pool) and
+    // the launch's kernel id
+    size_t timedLaunches = 0;
     std::vector<hipEvent_t> marks;
+    std::vector<int> markKernel;
 
     Dev dev() const
     {
@@ -583,13 +647,10 @@ void freeAll(carl_env* e)
     if (e->stream) (void)hipStreamDestroy(e->stream);
 }
 
-constexpr int kMarksPerTick = CARL_TICK_KERNELS + 1;
-
-// Timing marker i of the current tick (events are created on first use).
-int mark(carl_env* e, int i)
+// Timing events of the current timed launch: begin before it, end after it,
+// both on the environment stream (events are created on first use).
+int markEvent(carl_env* e, size_t slot)
 {
-    if (!e->timing) return CARL_OK;
-    const size_t slot = e->timedTicks * kMarksPerTick + i;
     while (e->marks.size() <= slot) {
         hipEvent_t ev;
         HIP_TRY(hipEventCreate(&ev));
@@ -599,16 +660,34 @@ int mark(carl_env* e, int i)
     return CARL_OK;
 }
 
-#define CARL_MARK(i)                      \
+int markBegin(carl_env* e, int kernel)
+{
+    if (!e->timing) return CARL_OK;
+    if (e->markKernel.size() <= e->timedLaunches) e->markKernel.resize(e->timedLaunches + 1);
+    e->markKernel[e->timedLaunches] = kernel;
+    return markEvent(e, 2 * e->timedLaunches);
+}
+
+int markEnd(carl_env* e)
+{
+    if (!e->timing) return CARL_OK;
+    const int rc = markEvent(e, 2 * e->timedLaunches + 1);
+    e->timedLaunches++;
+    return rc;
+}
+
+#define CARL_MARK(expr)                   \
     do {                                  \
-        const int rc_ = mark(e, (i));     \
+        const int rc_ = (expr);           \
         if (rc_ != CARL_OK) return rc_;   \
     } while (0)
 
 // Ticks run as e->tickStreams partitions of the simulations, partition 0 on
 // the environment stream and the others on auxiliary streams forked from and
-// joined back into it; the partitions share no data within a tick.  Timing
-// markers bracket partition 0's kernels.
+// joined back into it; the partitions share no data within a tick.  With
+// windowSims > 0 each partition runs all n ticks in one tick-window launch,
+// otherwise four phase kernels per tick.  Timing events bracket partition
+// 0's launches.
 int launchTicks(carl_env* e, int kind, const void* actions, int n)
 {
     if (n <= 0) return CARL_OK;
@@ -625,24 +704,37 @@ int launchTicks(carl_env* e, int kind, const void* actions, int n)
         HIP_TRY(hipEventRecord(e->fork, e->stream));
         for (int p = 1; p < parts; p++) HIP_TRY(hipStreamWaitEvent(stream[p], e->fork, 0));
     }
-    for (int k = 0; k < n; k++) {
+    if (e->windowSims > 0) {
+        const int wsb = std::min(e->windowSims, kWindowBlock / e->nCars);
+        for (int p = 0; p < parts; p++) {
+            const SimRange r = range[p];
+            const bool timed = p == 0;
+            if (timed) CARL_MARK(markBegin(e, CARL_KERNEL_WINDOW));
+            tickWindowKernel<<<e->grid(r.end - r.begin, wsb), kWindowBlock, 0, stream[p]>>>(
+                d, e->ws, e->contactScreen, kind, actions, e->tickCount + 1, n, wsb, r);
+            if (timed) CARL_MARK(markEnd(e));
+        }
+    }
+    for (int k = 0; e->windowSims == 0 && k < n; k++) {
         const int tick = e->tickCount + k + 1;
         for (int p = 0; p < parts; p++) {
             const SimRange r = range[p];
             const int sims = r.end - r.begin, cars = sims * e->nCars;
             hipStream_t st = stream[p];
             const bool timed = p == 0;
-            if (timed) CARL_MARK(CARL_KERNEL_CONTACT);
+            if (timed) CARL_MARK(markBegin(e, CARL_KERNEL_CONTACT));
             contactKernel<<<e->grid(cars, kContactOwners), kContactBlock, 0, st>>>(d, e->ws, e->contactScreen, r);
-            if (timed) CARL_MARK(CARL_KERNEL_CAR_ARENA);
+            if (timed) CARL_MARK(markEnd(e));
+            if (timed) CARL_MARK(markBegin(e, CARL_KERNEL_CAR_ARENA));
             carArenaKernel<<<e->grid(cars, kTickBlock), kTickBlock, 0, st>>>(d, e->ws, kind, actions, tick, r);
-            if (timed) CARL_MARK(CARL_KERNEL_BALL);
+            if (timed) CARL_MARK(markEnd(e));
+            if (timed) CARL_MARK(markBegin(e, CARL_KERNEL_BALL));
             ballKernel<<<e->grid(sims, kBallOwners), kBallBlock, 0, st>>>(d, tick, r);
-            if (timed) CARL_MARK(CARL_KERNEL_FINISH);
+            if (timed) CARL_MARK(markEnd(e));
+            if (timed) CARL_MARK(markBegin(e, CARL_KERNEL_FINISH));
             finishKernel<<<e->grid(sims, spb), spb * e->nCars, 0, st>>>(d, spb, r);
-            if (timed) CARL_MARK(CARL_TICK_KERNELS);
+            if (timed) CARL_MARK(markEnd(e));
         }
-        if (e->timing) e->timedTicks++;
     }
     HIP_TRY(hipGetLastError());
     for (int p = 1; p < parts; p++) {
@@ -1063,6 +1155,10 @@ int carl_env_set_param(carl_env* e, int p, int v)
         if (v != 0 && v != 1) return fail(CARL_ERR_VALUE, "contact_screen must be 0 or 1");
         e->contactScreen = v;
         return CARL_OK;
+    case CARL_PARAM_TICK_WINDOW:
+        if (v < 0 || v > kWindowBlock) return fail(CARL_ERR_VALUE, "tick_window must be in [0, 256]");
+        e->windowSims = v;
+        return CARL_OK;
     default: return fail(CARL_ERR_VALUE, "parameter is read-only or unknown");
     }
 }
@@ -1085,6 +1181,7 @@ int carl_env_get_param(carl_env* e, int p, int* v)
     case CARL_PARAM_N_BLUE: *v = e->nBlue; break;
     case CARL_PARAM_TICK_STREAMS: *v = e->tickStreams; break;
     case CARL_PARAM_CONTACT_SCREEN: *v = e->contactScreen; break;
+    case CARL_PARAM_TICK_WINDOW: *v = e->windowSims; break;
     default: return fail(CARL_ERR_VALUE, "unknown parameter");
     }
     return CARL_OK;
@@ -1095,7 +1192,7 @@ int carl_env_enable_timing(carl_env* e, int enable)
     CARL_TRY(checkEnv(e));
     HIP_TRY(hipStreamSynchronize(e->stream));
     e->timing = enable != 0;
-    e->timedTicks = 0;
+    e->timedLaunches = 0;
     return CARL_OK;
 }
 
@@ -1106,22 +1203,22 @@ int carl_env_tick_timing(carl_env* e, double* kernelMs, int* launches)
     HIP_TRY(hipStreamSynchronize(e->stream));
     for (int k = 0; k < CARL_TICK_KERNELS; k++) {
         kernelMs[k] = 0.0;
-        launches[k] = (int)e->timedTicks;
+        launches[k] = 0;
     }
-    for (size_t t = 0; t < e->timedTicks; t++) {
-        for (int k = 0; k < CARL_TICK_KERNELS; k++) {
-            float ms = 0.f;
-            HIP_TRY(hipEventElapsedTime(&ms, e->marks[t * kMarksPerTick + k], e->marks[t * kMarksPerTick + k + 1]));
-            kernelMs[k] += ms;
-        }
+    for (size_t i = 0; i < e->timedLaunches; i++) {
+        float ms = 0.f;
+        HIP_TRY(hipEventElapsedTime(&ms, e->marks[2 * i], e->marks[2 * i + 1]));
+        kernelMs[e->markKernel[i]] += ms;
+        launches[e->markKernel[i]]++;
     }
-    e->timedTicks = 0;
+    e->timedLaunches = 0;
     return CARL_OK;
 }
 
 const char* carl_tick_kernel_name(int kernel)
 {
-    static const char* names[CARL_TICK_KERNELS] = { "contactKernel", "carArenaKernel", "ballKernel", "finishKernel" };
+    static const char* names[CARL_TICK_KERNELS] = { "contactKernel", "carArenaKernel", "ballKernel", "finishKernel",
+                                                    "tickWindowKernel" };
     return kernel >= 0 && kernel < CARL_TICK_KERNELS ? names[kernel] : "";
 }
 

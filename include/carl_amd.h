@@ -110,10 +110,13 @@ enum {
     CARL_PARAM_TICK_COUNT = 9,   /* read-only: global physics tick counter */
     CARL_PARAM_N_BLUE = 10,      /* read-only */
     CARL_PARAM_TICK_STREAMS = 11, /* partitions of the simulations, each ticked on its own stream [1, 4];
-                                     no reference counterpart (default 4) */
-    CARL_PARAM_CONTACT_SCREEN = 12 /* 1: the contact search drops (car, triangle) pairs its float tests
+                                     no reference counterpart (default 1) */
+    CARL_PARAM_CONTACT_SCREEN = 12, /* 1: the contact search drops (car, triangle) pairs its float tests
                                       provably reject before running them; 0: it runs them on every pair.
                                       Results are identical; no reference counterpart (default 1) */
+    CARL_PARAM_TICK_WINDOW = 13    /* > 0: all ticks of a step in one launch per partition, this many
+                                      simulations per workgroup (at most 256 cars; default 128); 0: four phase kernels
+                                      per tick.  Results are identical; no reference counterpart */
 };
 
 /* ---- persistent state layout (export / import) ------------------------
@@ -288,15 +291,17 @@ int carl_env_import_state(carl_env* env, const uint32_t* car_state,
                           const uint32_t* sim_state, int tick_count);
 
 /* ---- tick-kernel timing (no reference counterpart) -------------------------
- * One physics tick is four kernels on the environment stream, in this order
- * (the reference's eleven per-tick launches, src/RLEnvironment.cu:166-211,
- * grouped by the data they own). */
+ * One physics tick is four phases, in this order (the reference's eleven
+ * per-tick launches, src/RLEnvironment.cu:166-211, grouped by the data they
+ * own): four kernels per tick, or one tick-window kernel running every phase
+ * of every tick of a step (CARL_PARAM_TICK_WINDOW). */
 enum {
     CARL_KERNEL_CONTACT = 0,    /* broadphase, wheel rays, car-arena contact search */
     CARL_KERNEL_CAR_ARENA = 1,  /* controls, suspension, car-arena solve */
     CARL_KERNEL_BALL = 2,       /* episode clock, car-car pairs, ball-arena, car-ball, goal */
     CARL_KERNEL_FINISH = 3,     /* integration, impulse caches, boost pads */
-    CARL_TICK_KERNELS = 4
+    CARL_KERNEL_WINDOW = 4,     /* all four phases of every tick of an env step, one launch */
+    CARL_TICK_KERNELS = 5
 };
 
 /* With timing enabled, HIP events recorded on the environment stream bracket

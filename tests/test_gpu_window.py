@@ -1,0 +1,74 @@
+"""The tick-window kernel changes no result.
+
+With CARL_PARAM_TICK_WINDOW > 0 a step's ticks run in one launch per
+partition, a workgroup taking every phase of every tick for its own
+simulations; with 0 they run as four phase kernels per tick.  These tests run
+both on identical inputs and require every field of the persistent state and
+every packed output to agree bit for bit, over team sizes, workgroup sizes,
+partition counts and frameskips, at sizes the oracle cannot reach.
+"""
+import numpy as np
+import pytest
+import torch
+
+import carl_amd
+from carl_amd import workloads
+from gpu_harness import dense_geometry_reset_state, describe_mismatch, dev, gpu_state
+from abi import CAR_NAMES, SIM_NAMES
+
+pytestmark = pytest.mark.gpu
+
+
+def _run_both(n, n_blue, n_orange, frameskip, steps, make_state, seed, window=64, streams=4, reset_every=0):
+    rng = np.random.default_rng(seed)
+    nc = n_blue + n_orange
+    fused = carl_amd.Env(n, n_blue, n_orange, 5, frameskip, True, False, True)
+    phased = carl_amd.Env(n, n_blue, n_orange, 5, frameskip, True, False, True)
+    fused.tick_window = window
+    fused.tick_streams = streams
+    phased.tick_window = 0
+    phased.tick_streams = streams
+    assert (fused.tick_window, phased.tick_window) == (window, 0)
+    state = {k: dev(v) for k, v in make_state(rng, n, nc).items()}
+    for env in (fused, phased):
+        env.apply_reset_state(**state)
+    for step in range(steps):
+        if reset_every and step % reset_every == 0:
+            mask = dev(rng.uniform(size=n) < 0.25)
+            fresh = {k: dev(v) for k, v in make_state(rng, n, nc).items()}
+            for env in (fused, phased):
+                env.apply_reset_state(**fresh, reset_mask=mask)
+        actions = dev(workloads.random_continuous_actions(rng, n, nc))
+        fused.step_continuous(actions)
+        phased.step_continuous(actions)
+        a, b = gpu_state(fused), gpu_state(phased)
+        report = describe_mismatch(CAR_NAMES, a[0], b[0]) + describe_mismatch(SIM_NAMES, a[1], b[1])
+        for name in ("get_obs", "get_state", "get_rewards", "get_dones"):
+            x = torch.from_dlpack(getattr(fused, name)()).cpu().numpy()
+            y = torch.from_dlpack(getattr(phased, name)()).cpu().numpy()
+            if x.tobytes() != y.tobytes():
+                report.append(f"{name} differs")
+        if report:
+            pytest.fail(f"window {window} vs phase kernels after step {step}:\n  " + "\n  ".join(report))
+
+
+def test_window_random_states_1v1(gpu):
+    _run_both(8192, 1, 1, 8, 30, workloads.random_reset_state, seed=41)
+
+
+@pytest.mark.parametrize("window,streams", [(16, 4), (128, 1), (37, 3)])
+def test_window_block_sizes_and_partitions(gpu, window, streams):
+    _run_both(3001, 1, 1, 8, 12, workloads.random_reset_state, seed=42, window=window, streams=streams)
+
+
+def test_window_dense_geometry_3v3_and_2v2(gpu):
+    _run_both(1024, 3, 3, 4, 20, dense_geometry_reset_state, seed=43)
+    _run_both(2048, 2, 2, 4, 20, dense_geometry_reset_state, seed=44, window=32)
+
+
+def test_window_per_tick_steps_with_masked_resets(gpu):
+    _run_both(4096, 2, 2, 1, 40, workloads.random_reset_state, seed=45, reset_every=1)
+
+
+def test_window_single_car(gpu):
+    _run_both(1000, 1, 0, 8, 15, workloads.random_reset_state, seed=46)
