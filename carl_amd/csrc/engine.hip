@@ -79,6 +79,7 @@ static_assert(kContactOwners <= kContactBlock, "owners are lanes of the block");
 // The contact search of cars [car0, car0 + kContactOwners) (those below
 // carEnd) by one wave; L is that wave's own LDS.  Every lane of the wave calls
 // it; it synchronises the wave only.
+template <int Depth>
 DI void contactGroup(const Dev& d, uint32_t* __restrict__ ws, int screen, int car0, int carEnd, ContactLds& L, int lane)
 {
     const int car = car0 + lane;
@@ -95,7 +96,7 @@ DI void contactGroup(const Dev& d, uint32_t* __restrict__ ws, int screen, int ca
     }
     contactPrepare(L, lane, ok && !demoed, cen, rot, bp.start, screen != 0);
     waveSync();
-    waveItemsPipelined(
+    waveItemsDeep<Depth>(
         bp.count, L.excl, [&](int o, int q, bool valid) { return contactFetch(d, L, o, q, valid); },
         [&](const RefBox& b, int o, int q, int) { contactScreen(L, b, o, q, lane); },
         [&](bool last) { contactDrain(d, L, lane, last); });
@@ -122,8 +123,8 @@ DI void contactGroup(const Dev& d, uint32_t* __restrict__ ws, int screen, int ca
 __global__ __launch_bounds__(kContactBlock) void contactKernel(Dev d, uint32_t* __restrict__ ws, int screen, SimRange range)
 {
     __shared__ ContactLds L;
-    contactGroup(d, ws, screen, range.begin * d.nCars + blockIdx.x * kContactOwners, range.end * d.nCars, L,
-                 threadIdx.x);
+    contactGroup<1>(d, ws, screen, range.begin * d.nCars + blockIdx.x * kContactOwners, range.end * d.nCars, L,
+                    threadIdx.x);
 }
 
 // A2: controls, car-arena contacts, suspension and the contact solve.
@@ -276,6 +277,11 @@ __global__ __launch_bounds__(kTickBlock) void finishKernel(Dev d, int simsPerBlo
 constexpr int kWindowBlock = 256;
 constexpr int kWindowWaves = kWindowBlock / 64;
 constexpr int kDefaultWindowSims = 128;
+// rounds of candidate loads the window kernel's contact search keeps in flight
+#ifndef CARL_WINDOW_CONTACT_DEPTH
+#define CARL_WINDOW_CONTACT_DEPTH 1
+#endif
+constexpr int kWindowContactDepth = CARL_WINDOW_CONTACT_DEPTH;
 
 union WindowLds {
     ContactLds contact[kWindowWaves];
@@ -295,7 +301,7 @@ __global__ __launch_bounds__(kWindowBlock, 2) void tickWindowKernel(Dev d, uint3
     for (int k = 0; k < ticks; k++) {
         const int tick = tick0 + k;
         for (int g = car0 + wave * kContactOwners; g < carEnd; g += kWindowWaves * kContactOwners)
-            contactGroup(d, ws, screen, g, carEnd, L.contact[wave], lane);
+            contactGroup<kWindowContactDepth>(d, ws, screen, g, carEnd, L.contact[wave], lane);
         __syncthreads();
         for (int c = car0 + t; c < carEnd; c += kWindowBlock) carArenaCar(d, ws, kind, actions, tick, c);
         __syncthreads();

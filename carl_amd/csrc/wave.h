@@ -100,6 +100,56 @@ __device__ __forceinline__ void waveItemsPipelined(int count, int* excl, Fetch&&
     }
 }
 
+// waveItemsPipelined with the loads of the next D rounds in flight: a ring of
+// D fetched rounds, the loop unrolled by D so every slot is a register.
+// Same visiting order, lane placement and hooks as waveItemsPipelined (which
+// is D = 1).
+template <int D, typename Fetch, typename Process, typename After>
+__device__ __forceinline__ void waveItemsDeep(int count, int* excl, Fetch&& fetch, Process&& process, After&& after)
+{
+    const int lane = (int)(threadIdx.x & 63);
+    const int incl = waveInclusiveScan(count);
+    const int total = __builtin_amdgcn_readlane(incl, 63);
+    excl[lane] = incl - count;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (total == 0) return;
+    auto locate = [&](int j, int& o, int& q) {
+        o = 0;
+        q = 0;
+        if (j < total) {
+#pragma unroll
+            for (int step = 32; step > 0; step >>= 1)
+                if (excl[o + step] <= j) o += step;
+            q = j - excl[o];
+        }
+    };
+    using Value = decltype(fetch(0, 0, false));
+    Value buf[D];
+    int os[D], qs[D];
+#pragma unroll
+    for (int r = 0; r < D; r++) {
+        locate(r * 64 + lane, os[r], qs[r]);
+        buf[r] = fetch(os[r], qs[r], r * 64 + lane < total);
+    }
+    for (int base = 0; base < total;) {
+#pragma unroll
+        for (int r = 0; r < D; r++) {
+            if (base < total) {
+                const Value cur = buf[r];
+                const int o = os[r], q = qs[r];
+                const int jn = base + D * 64 + lane;
+                locate(jn, os[r], qs[r]);
+                buf[r] = fetch(os[r], qs[r], jn < total);
+                if (base + lane < total) process(cur, o, q, base);
+                after(base + 64 >= total);   // every lane; true after the last round
+                base += 64;
+            }
+        }
+    }
+}
+
 // Without a per-round hook.
 template <typename Fetch, typename Process>
 __device__ __forceinline__ void waveItemsPipelined(int count, int* excl, Fetch&& fetch, Process&& process)
