@@ -74,11 +74,11 @@ def kernel_bytes(kernel: str, n_cars: int, ticks: int) -> int:
 TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_1v1_n65536_ts8.md"
 
 
-def measured_traffic(kernel: str, n_sim: int, n_cars: int, tick_skip: int, parts: int):
+def measured_traffic(kernel: str, n_sim: int, n_cars: int, tick_skip: int, parts: int, window: int):
     """HBM bytes per dispatch of `kernel` from the committed rocprofv3
     FETCH_SIZE / WRITE_SIZE summary of the headline workload (copy-calibrated);
     None for any other workload or when the summary is absent."""
-    if (n_sim, n_cars, tick_skip, parts) != (65536, 2, 8, 4) or not TRAFFIC_FILE.is_file():
+    if (n_sim, n_cars, tick_skip, parts, window) != (65536, 2, 8, 1, 128) or not TRAFFIC_FILE.is_file():
         return None
     for line in TRAFFIC_FILE.read_text().splitlines():
         f = line.split()
@@ -234,7 +234,7 @@ def main() -> None:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": measured_traffic(kernel, n_sim, n_cars, args.tick_skip, parts),
+            "traffic": measured_traffic(kernel, n_sim, n_cars, args.tick_skip, parts, env.tick_window),
             "traffic_source": TRAFFIC_FILE.name,
             "launch_ms": launch_ms,
             "launches": launches,
