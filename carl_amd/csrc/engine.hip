@@ -350,71 +350,137 @@ __global__ void matchKernel(Dev d, int* score, int* ticks, bool* overtime, const
 }
 
 // Row-major outputs (observations, canonical states) are written through
-// LDS: each lane builds one row there, then the wave stores the block's rows
-// as one contiguous run, so each store instruction covers consecutive words.
-// A lane storing its own row would touch a different line per lane and per
-// store, and lines evicted half-written cost extra HBM writes.  Rows are at
-// least kPackBlock words long (the shortest is the 1-car state, 65), so the
-// row/column position of a lane advances by at most one row per round.
-// A block stages at most kPackLdsBytes of rows (16 rows of a 1v1
-// observation): the row-building phase is latency-bound, and small blocks
-// keep more of them resident per CU (measured 40 KB -> 10 KB: +2% per env step).
-constexpr int kPackBlock = 64;
-constexpr int kPackLdsBytes = 10 * 1024;
+// LDS.  A packing workgroup is four waves; rows go in chunks of up to 64, and
+// wave q builds column part q (packObservationPart / packStatePart) of every
+// row of the chunk, one row per lane, at an odd stride so the lanes' writes
+// fall in distinct banks.  The workgroup then stores the chunk's rows as one
+// contiguous run, so each store instruction covers consecutive words (a lane
+// storing its own row touched a different line per lane and per store).
+constexpr int kPackBlock = 64 * kRowParts;
+constexpr int kPackLdsBytes = 38 * 1024;   // four workgroups per CU
 
-// odd row stride: the lanes' row writes fall in distinct LDS banks
 HDI int packStride(int rowLen) { return rowLen | 1; }
-HDI int packRowsPerBlock(int rowLen)
+HDI int packChunkRows(int rowLen)
 {
-    int rows = kPackBlock;
+    int rows = 64;
     while (rows > 8 && rows * packStride(rowLen) * 4 > kPackLdsBytes) rows /= 2;
     return rows;
 }
+HDI size_t packLdsBytes(int rowLen) { return (size_t)packChunkRows(rowLen) * packStride(rowLen) * sizeof(float); }
 
-static_assert(stateDim(1) > kPackBlock && observationDim(1, false) > kPackBlock,
-              "packRows steps a lane by less than one row per round");
-
-// Rows [r0, r0 + rowsPerBlock) of out (nRows rows of rowLen floats); row r is
-// built by row(r, dst) when simMask is null or simMask[r / rowsPerSim] is set,
-// and only those rows are stored.
-template <typename Row>
-DI void packRows(float* out, int rowLen, int nRows, int rowsPerBlock, const bool* simMask, int rowsPerSim, Row&& row)
+// Rows [r0, r1) of out (rowLen floats each): a row r with keep(r) is built by
+// part(r, q, dst) for q = 0..kRowParts-1 and stored; other rows are left
+// untouched.  Every thread of the workgroup calls this (it holds barriers);
+// on return every part() call of the workgroup has completed.
+template <typename Keep, typename Part>
+DI void packRowsParts(float* out, int rowLen, int r0, int r1, Keep&& keep, Part&& part)
 {
     extern __shared__ float packLds[];
-    __shared__ int on[kPackBlock];
-    const int lane = threadIdx.x;
-    const int stride = packStride(rowLen);
-    const int r0 = blockIdx.x * rowsPerBlock;
-    const int r = r0 + lane;
-    const bool mine = lane < rowsPerBlock && r < nRows && (!simMask || simMask[r / rowsPerSim]);
-    if (!__any(mine)) return;   // whole wave: no row of this block is packed
-    if (mine) row(r, packLds + lane * stride);
-    on[lane] = mine;
-    __syncthreads();
-    const int rows = min(rowsPerBlock, nRows - r0);
-    const int total = rows * rowLen;
-    float* dst = out + (size_t)r0 * rowLen;
-    int rr = 0, c = lane;
-    for (int e = lane; e < total; e += kPackBlock) {
-        if (on[rr]) dst[e] = packLds[rr * stride + c];
-        c += kPackBlock;
-        if (c >= rowLen) { c -= rowLen; rr++; }
+    __shared__ int on[64];
+    const int t = threadIdx.x, lane = t & 63, q = t >> 6;
+    const int stride = packStride(rowLen), chunk = packChunkRows(rowLen);
+    const int rowStep = kPackBlock / rowLen, colStep = kPackBlock % rowLen;
+    for (int c0 = r0; c0 < r1; c0 += chunk) {
+        const int rows = min(chunk, r1 - c0);
+        const bool mine = lane < rows && keep(c0 + lane);
+        if (q == 0) on[lane] = mine;
+        if (!__syncthreads_or(mine)) continue;
+        if (mine) part(c0 + lane, q, packLds + lane * stride);
+        __syncthreads();
+        float* dst = out + (size_t)c0 * rowLen;
+        int rr = t / rowLen, c = t % rowLen;
+        for (int e = t; e < rows * rowLen; e += kPackBlock) {
+            if (on[rr]) dst[e] = packLds[rr * stride + c];
+            rr += rowStep;
+            c += colStep;
+            if (c >= rowLen) { c -= rowLen; rr++; }
+        }
+        __syncthreads();
     }
 }
 
-__global__ __launch_bounds__(kPackBlock) void stateKernel(Dev d, float* out, int stateDimV, int rowsPerBlock,
-                                                         int touchWindow, int tickCount, const bool* mask)
+__global__ __launch_bounds__(kPackBlock) void stateKernel(Dev d, float* out, int stateDimV, int touchWindow,
+                                                         int tickCount, const bool* mask)
 {
-    packRows(out, stateDimV, d.nSim, rowsPerBlock, mask, 1,
-             [&](int s, float* o) { packStateRow(d, s, touchWindow, tickCount, o); });
+    const int r0 = blockIdx.x * packChunkRows(stateDimV);
+    packRowsParts(
+        out, stateDimV, r0, min(r0 + packChunkRows(stateDimV), d.nSim), [&](int s) { return !mask || mask[s]; },
+        [&](int s, int q, float* o) { packStatePart(d, s, touchWindow, tickCount, q, o); });
 }
 
-__global__ __launch_bounds__(kPackBlock) void obsKernel(Dev d, float* out, int obsDimV, int rowsPerBlock,
-                                                       const bool* mask, int invert, int normalizeObs, int prev)
+__global__ __launch_bounds__(kPackBlock) void obsKernel(Dev d, float* out, int obsDimV, const bool* mask, int invert,
+                                                       int normalizeObs, int prev)
 {
-    packRows(out, obsDimV, d.nTotal, rowsPerBlock, mask, d.nCars, [&](int a, float* o) {
-        packObservation(d, a / d.nCars, a % d.nCars, invert != 0, normalizeObs != 0, prev != 0, o);
-    });
+    const int r0 = blockIdx.x * packChunkRows(obsDimV);
+    packRowsParts(
+        out, obsDimV, r0, min(r0 + packChunkRows(obsDimV), d.nTotal),
+        [&](int a) { return !mask || mask[a / d.nCars]; },
+        [&](int a, int q, float* o) {
+            packObservationPart(d, a / d.nCars, a % d.nCars, invert != 0, normalizeObs != 0, prev != 0, q, o);
+        });
+}
+
+// Everything an env step does after its ticks, for kStepSims simulations per
+// workgroup, in the reference's order: rewards and dones, the transition
+// state and the transition observations of finished simulations, their
+// resets, the match state, the observations and the state.  A simulation's
+// rows depend on nothing but its own state, so the workgroup needs only its
+// own barriers between the stages.
+constexpr int kStepSims = 64;
+
+struct StepIO {
+    float *rewards, *tstate, *tobs, *obs, *state;
+    bool *dones, *tovertime, *overtime;
+    int32_t *tscore, *tticks, *score, *ticks;
+    const uint32_t* actions;  // the step's actions, 7 words per car ...
+    uint32_t* actionCopy;     // ... kept here (null: not kept)
+    int obsDim, stateDim, invert, normalize, prev, frameskip, tickCount, nOrange;
+    DoneRule rule;
+};
+
+__global__ __launch_bounds__(kPackBlock) void stepEnvKernel(Dev d, StepIO io)
+{
+    __shared__ int done[kStepSims];
+    const int t = threadIdx.x, nC = d.nCars;
+    const int s0 = blockIdx.x * kStepSims, s1 = min(s0 + kStepSims, d.nSim);
+    const int s = s0 + t;
+    if (io.actionCopy) {
+        const size_t w0 = (size_t)s0 * nC * 7;
+        for (int w = t; w < (s1 - s0) * nC * 7; w += kPackBlock) io.actionCopy[w0 + w] = io.actions[w0 + w];
+    }
+    if (s < s1) {
+        const bool dn = simDone(d, s, io.tickCount, io.rule);
+        io.rewards[s] = (float)d.si(CARL_SIM_LAST_SCORER, s);
+        io.dones[s] = dn;
+        io.tscore[s] = d.si(CARL_SIM_BLUE_SCORE, s) - d.si(CARL_SIM_ORANGE_SCORE, s);
+        io.tticks[s] = d.si(CARL_SIM_EPISODE_TICKS, s);
+        io.tovertime[s] = d.si(CARL_SIM_OVERTIME, s) != 0;
+        done[t] = dn;
+    }
+    __syncthreads();
+    packRowsParts(
+        io.tstate, io.stateDim, s0, s1, [](int) { return true; },
+        [&](int r, int q, float* o) { packStatePart(d, r, io.frameskip, io.tickCount, q, o); });
+    packRowsParts(
+        io.tobs, io.obsDim, s0 * nC, s1 * nC, [&](int a) { return done[a / nC - s0] != 0; },
+        [&](int a, int q, float* o) {
+            packObservationPart(d, a / nC, a % nC, io.invert != 0, io.normalize != 0, io.prev != 0, q, o);
+        });
+    if (s < s1) resetAfterDone(d, s, io.tickCount, io.rule, io.nOrange);
+    __syncthreads();
+    if (s < s1) {
+        io.score[s] = d.si(CARL_SIM_BLUE_SCORE, s) - d.si(CARL_SIM_ORANGE_SCORE, s);
+        io.ticks[s] = d.si(CARL_SIM_EPISODE_TICKS, s);
+        io.overtime[s] = d.si(CARL_SIM_OVERTIME, s) != 0;
+    }
+    packRowsParts(
+        io.obs, io.obsDim, s0 * nC, s1 * nC, [](int) { return true; },
+        [&](int a, int q, float* o) {
+            packObservationPart(d, a / nC, a % nC, io.invert != 0, io.normalize != 0, io.prev != 0, q, o);
+        });
+    packRowsParts(
+        io.state, io.stateDim, s0, s1, [](int) { return true; },
+        [&](int r, int q, float* o) { packStatePart(d, r, 1, io.tickCount, q, o); });
 }
 
 __global__ void setBallKernel(Dev d, const float* pos, const float* vel, const float* ang, Selection sel)
@@ -753,20 +819,16 @@ int launchTicks(carl_env* e, int kind, const void* actions, int n)
 
 int packObs(carl_env* e, float* out, const bool* mask)
 {
-    const int rows = packRowsPerBlock(e->obsDim);
-    const size_t lds = (size_t)rows * packStride(e->obsDim) * sizeof(float);
-    obsKernel<<<e->grid(e->nTotal, rows), kPackBlock, lds, e->stream>>>(e->dev(), out, e->obsDim, rows, mask, e->invert,
-                                                                       e->normalize, e->prevControls);
+    obsKernel<<<e->grid(e->nTotal, packChunkRows(e->obsDim)), kPackBlock, packLdsBytes(e->obsDim), e->stream>>>(
+        e->dev(), out, e->obsDim, mask, e->invert, e->normalize, e->prevControls);
     HIP_TRY(hipGetLastError());
     return CARL_OK;
 }
 
 int packState(carl_env* e, float* out, int touchWindow, const bool* mask)
 {
-    const int rows = packRowsPerBlock(e->stateDim);
-    const size_t lds = (size_t)rows * packStride(e->stateDim) * sizeof(float);
-    stateKernel<<<e->grid(e->nSim, rows), kPackBlock, lds, e->stream>>>(e->dev(), out, e->stateDim, rows, touchWindow,
-                                                                       e->tickCount, mask);
+    stateKernel<<<e->grid(e->nSim, packChunkRows(e->stateDim)), kPackBlock, packLdsBytes(e->stateDim), e->stream>>>(
+        e->dev(), out, e->stateDim, touchWindow, e->tickCount, mask);
     HIP_TRY(hipGetLastError());
     return CARL_OK;
 }
@@ -1004,25 +1066,24 @@ int carl_env_step(carl_env* e, int kind, const void* actions)
 {
     CARL_TRY(checkEnv(e));
     if (!actions) return fail(CARL_ERR_VALUE, "null actions");
-    const void* src = actions;
-    const size_t bytes = (size_t)e->nTotal * 7 * 4;
-    if (kind == CARL_ACTIONS_DISCRETE) {
-        HIP_TRY(hipMemcpyAsync(e->actions, actions, bytes, hipMemcpyDeviceToDevice, e->stream));
-        src = e->actions;
-    } else if (kind == CARL_ACTIONS_CONTINUOUS) {
-        HIP_TRY(hipMemcpyAsync(e->cactions, actions, bytes, hipMemcpyDeviceToDevice, e->stream));
-        src = e->cactions;
-    } else if (kind != CARL_ACTIONS_DIRECT) {
-        return fail(CARL_ERR_VALUE, "unknown action kind");
-    }
-    CARL_TRY(launchTicks(e, kind, src, e->frameskip));
-    CARL_TRY(packRewardsDones(e));
-    CARL_TRY(packState(e, e->tstate, e->frameskip, nullptr));
-    CARL_TRY(packObs(e, e->tobs, e->dones));
-    CARL_TRY(carl_env_reset_dones(e));
-    CARL_TRY(packMatch(e, nullptr));
-    CARL_TRY(packObs(e, e->obs, nullptr));
-    CARL_TRY(packState(e, e->state, 1, nullptr));
+    uint32_t* keep = nullptr;
+    if (kind == CARL_ACTIONS_DISCRETE) keep = (uint32_t*)e->actions;
+    else if (kind == CARL_ACTIONS_CONTINUOUS) keep = (uint32_t*)e->cactions;
+    else if (kind != CARL_ACTIONS_DIRECT) return fail(CARL_ERR_VALUE, "unknown action kind");
+    CARL_TRY(launchTicks(e, kind, actions, e->frameskip));
+    StepIO io{};
+    io.rewards = e->rewards; io.tstate = e->tstate; io.tobs = e->tobs; io.obs = e->obs; io.state = e->state;
+    io.dones = e->dones; io.tovertime = e->tovertime; io.overtime = e->overtime;
+    io.tscore = e->tscore; io.tticks = e->tticks; io.score = e->score; io.ticks = e->ticks;
+    io.actions = (const uint32_t*)actions;
+    io.actionCopy = keep == actions ? nullptr : keep;
+    io.obsDim = e->obsDim; io.stateDim = e->stateDim;
+    io.invert = e->invert; io.normalize = e->normalize; io.prev = e->prevControls;
+    io.frameskip = e->frameskip; io.tickCount = e->tickCount; io.nOrange = e->nOrange;
+    io.rule = e->rule();
+    const size_t lds = std::max(packLdsBytes(e->obsDim), packLdsBytes(e->stateDim));
+    stepEnvKernel<<<e->grid(e->nSim, kStepSims), kPackBlock, lds, e->stream>>>(e->dev(), io);
+    HIP_TRY(hipGetLastError());
     return CARL_OK;
 }
 

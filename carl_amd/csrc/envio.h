@@ -40,16 +40,41 @@ DI void packCar(const Dev& d, int c, bool inv, float* o, int& k)
     o[k++] = (float)d.ci(CARL_CAR_IS_BOOSTING, c);
 }
 
-// one observer's row: ball, self, teammates, opponents, pads, relative
-// vectors, goals, dodge window, controller state [, previous controls]
-DI void packObservation(const Dev& d, int sim, int obs, bool invertOrange, bool normalizeObs, bool prev, float* o)
+// Rows are built in kRowParts column parts, one lane per part, so that the
+// four waves of a packing workgroup share every row's arithmetic.
+constexpr int kRowParts = 4;
+
+// Column of the first pad flag in an observation row (pad distances follow
+// the kPads flags).
+HDI int obsPadColumn(int nCars) { return 9 + nCars * kObsPerCar; }
+
+// Part `part` of one observer's row: ball, self, teammates, opponents, pads,
+// relative vectors, goals, dodge window, controller state [, previous
+// controls].  Part 0 writes every column except the pads' and normalises
+// them; part q > 0 writes the flag and the distance of the pads p with
+// p % 3 == q - 1.
+DI void packObservationPart(const Dev& d, int sim, int obs, bool invertOrange, bool normalizeObs, bool prev, int part,
+                            float* o)
 {
     const int nC = d.nCars, base = sim * nC;
     const bool orange = obs >= d.nBlue;
     const bool inv = invertOrange && orange;
     const int ego = base + obs;
+    const V3 egoPos = d.cv(CARL_CAR_POS, ego);
+    const int padCol = obsPadColumn(nC);
+    if (part > 0) {
+#pragma unroll
+        for (int p = 0; p < kPads; p++) {
+            if (p % 3 != part - 1) continue;
+            const int pi = inv ? mirroredPad(p) : p;
+            o[padCol + p] = d.sf(CARL_SIM_PAD_COOLDOWN + pi, sim) <= 0.f;
+            const float dist = len(egoPos - V3{ kPadPos[pi][0], kPadPos[pi][1], kPadPos[pi][2] });
+            o[padCol + kPads + p] = normalizeObs ? dist / 14692.54f : dist;
+        }
+        return;
+    }
     const V3 ballPos = d.sv(CARL_SIM_BALL_POS, sim), ballVel = d.sv(CARL_SIM_BALL_VEL, sim);
-    const V3 egoPos = d.cv(CARL_CAR_POS, ego), egoVel = d.cv(CARL_CAR_VEL, ego);
+    const V3 egoVel = d.cv(CARL_CAR_VEL, ego);
     int k = 0;
     put3(o, k, mirrorXY(ballPos, inv));
     put3(o, k, mirrorXY(ballVel, inv));
@@ -60,14 +85,7 @@ DI void packObservation(const Dev& d, int sim, int obs, bool invertOrange, bool 
     for (int c = tS; c < tE; c++)
         if (c != obs) packCar(d, base + c, inv, o, k);
     for (int c = oS; c < oE; c++) packCar(d, base + c, inv, o, k);
-    for (int p = 0; p < kPads; p++) {
-        const int pi = inv ? mirroredPad(p) : p;
-        o[k++] = d.sf(CARL_SIM_PAD_COOLDOWN + pi, sim) <= 0.f;
-    }
-    for (int p = 0; p < kPads; p++) {
-        const int pi = inv ? mirroredPad(p) : p;
-        o[k++] = len(egoPos - V3{ kPadPos[pi][0], kPadPos[pi][1], kPadPos[pi][2] });
-    }
+    k += 2 * kPads;
     put3(o, k, mirrorXY(ballPos - egoPos, inv));
     put3(o, k, mirrorXY(ballVel - egoVel, inv));
     for (int c = tS; c < tE; c++) {
@@ -113,9 +131,7 @@ DI void packObservation(const Dev& d, int sim, int obs, bool invertOrange, bool 
         for (int a = 6; a < 9; a++) o[off + a] /= kCarMaxAng;
         o[off + 15] /= kBoostMax;
     }
-    const int dOff = 9 + nC * kObsPerCar + kPads;
-    for (int p = 0; p < kPads; p++) o[dOff + p] /= 14692.54f;
-    int r = dOff + kPads;
+    int r = padCol + 2 * kPads;
     for (int a = 0; a < 3; a++) {
         o[r + a] /= 2.f * comp(scale, a);
         o[r + 3 + a] /= kBallMaxSpeed + kCarMaxSpeed;
@@ -132,18 +148,26 @@ DI void packObservation(const Dev& d, int sim, int obs, bool invertOrange, bool 
         for (int a = 0; a < 3; a++) o[r + g * 3 + a] /= 2.f * comp(scale, a);
 }
 
-DI void packStateRow(const Dev& d, int sim, int touchWindow, int tickCount, float* o)
+// Part `part` of a simulation's canonical state row (ball, cars, pad flags):
+// part 0 writes the ball and the pad flags, part q > 0 the cars c with
+// c % 3 == q - 1.
+DI void packStatePart(const Dev& d, int sim, int touchWindow, int tickCount, int part, float* o)
 {
-    int k = 0;
-    put3(o, k, d.sv(CARL_SIM_BALL_POS, sim));
-    put3(o, k, d.sv(CARL_SIM_BALL_VEL, sim));
-    put3(o, k, d.sv(CARL_SIM_BALL_ANG, sim));
-    for (int c = 0; c < d.nCars; c++) {
+    if (part == 0) {
+        int k = 0;
+        put3(o, k, d.sv(CARL_SIM_BALL_POS, sim));
+        put3(o, k, d.sv(CARL_SIM_BALL_VEL, sim));
+        put3(o, k, d.sv(CARL_SIM_BALL_ANG, sim));
+        k = 9 + d.nCars * kStatePerCar;
+        for (int p = 0; p < kPads; p++) o[k++] = d.sf(CARL_SIM_PAD_COOLDOWN + p, sim) <= 0.f;
+        return;
+    }
+    for (int c = part - 1; c < d.nCars; c += 3) {
         const int car = sim * d.nCars + c;
+        int k = 9 + c * kStatePerCar;
         packCar(d, car, false, o, k);
         o[k++] = d.ci(CARL_CAR_BALL_CONTACT_TICK, car) > tickCount - touchWindow;
     }
-    for (int p = 0; p < kPads; p++) o[k++] = d.sf(CARL_SIM_PAD_COOLDOWN + p, sim) <= 0.f;
 }
 
 struct DoneRule {

@@ -228,10 +228,12 @@ int carl_env_synchronize(carl_env* env);
 
 /* ---- stepping ------------------------------------------------------------ */
 
-/* One environment step: copies actions (device pointer, layout per kind) into
- * the environment's action buffer, runs `frameskip` physics ticks, then packs
- * rewards/dones, the transition state/obs, resets finished simulations and
- * packs the current obs/state (python/carl.cu:320-370). */
+/* One environment step: runs `frameskip` physics ticks on actions (device
+ * pointer, layout per kind), then packs rewards/dones, the transition
+ * state/obs, resets finished simulations, packs the current obs/state and
+ * leaves a copy of the actions in the environment's action buffer
+ * (python/carl.cu:320-370).  The work is queued on the environment stream;
+ * `actions` must stay unchanged until it has run. */
 int carl_env_step(carl_env* env, int kind, const void* actions);
 
 /* Physics ticks only, no packing (RLEnvironment::step). */
