@@ -311,7 +311,19 @@ __global__ __launch_bounds__(kWindowBlock, 2) void tickWindowKernel(Dev d, uint3
         for (int c = car0 + t; c < carEnd; c += kWindowBlock) finishCar(d, c);
         for (int s = sim0 + t; s < simEnd; s += kWindowBlock) finishBall(d, s);
         __syncthreads();
-        for (int s = sim0 + t; s < simEnd; s += kWindowBlock) boostPads(d, s);
+        {
+            // boost pads: the workgroup's threads split into kWindowBlock /
+            // simsPerBlock parts, each taking a contiguous range of every
+            // simulation's pads (in 1v1 two parts of two waves each).  The
+            // split is derived here from a copy of the thread index that the
+            // optimiser cannot hoist, so it holds no registers through the
+            // other phases.
+            int tp = t;
+            asm volatile("" : "+v"(tp));
+            const int parts = kWindowBlock / simsPerBlock, q = tp / simsPerBlock, j = tp - q * simsPerBlock;
+            if (q < parts && j < simEnd - sim0)
+                boostPadsRange(d, sim0 + j, kPads * q / parts, kPads * (q + 1) / parts);
+        }
         __syncthreads();
     }
 }

@@ -1092,7 +1092,14 @@ DI void finishBall(const Dev& d, int s)
 // pass (at most kMaxCars per simulation); boosts are written back once.
 constexpr int kMaxCars = 8;
 
-DI void boostPads(const Dev& d, int s)
+// Boost pads [p0, p1) of simulation s: cooldowns, pickups and the boost
+// they give.  No car position lies in two pads' cylinders (the closest pair
+// of cylinders is 773 uu apart), so a car takes boost from at most one pad per
+// tick: disjoint pad ranges of one simulation can run in different threads,
+// in any order, with the same result.  A thread reads every car's boost but
+// uses it only for a car inside one of its own pads, the only case in which
+// it writes that boost.
+DI void boostPadsRange(const Dev& d, int s, int p0, int p1)
 {
     const int base = s * d.nCars;
     V3 cp[kMaxCars];
@@ -1109,13 +1116,14 @@ DI void boostPads(const Dev& d, int s)
             boost[k] = d.cf(CARL_CAR_BOOST, base + k);
         }
     }
-    // all cooldowns are read before any is written back
+    // all cooldowns of the range are read before any is written back
     float cool[kPads];
 #pragma unroll
-    for (int p = 0; p < kPads; p++) cool[p] = d.sf(CARL_SIM_PAD_COOLDOWN + p, s);
+    for (int p = 0; p < kPads; p++) cool[p] = p >= p0 && p < p1 ? d.sf(CARL_SIM_PAD_COOLDOWN + p, s) : 0.f;
     int changed = 0;
 #pragma unroll
     for (int p = 0; p < kPads; p++) {
+        if (p < p0 || p >= p1) continue;
         const float prev = cool[p];
         float cd = prev;
         if (cd > 0.f) cd = fmax_(cd - kDt, 0.f);
@@ -1147,5 +1155,7 @@ DI void boostPads(const Dev& d, int s)
     for (int k = 0; k < kMaxCars; k++)
         if (changed & (1 << k)) d.setf(CARL_CAR_BOOST, base + k, boost[k]);
 }
+
+DI void boostPads(const Dev& d, int s) { boostPadsRange(d, s, 0, kPads); }
 
 }  // namespace carl
