@@ -115,7 +115,7 @@ enum {
                                       provably reject before running them; 0: it runs them on every pair.
                                       Results are identical; no reference counterpart (default 1) */
     CARL_PARAM_TICK_WINDOW = 13    /* > 0: all ticks of a step in one launch per partition, this many
-                                      simulations per workgroup (at most 256 cars; default 128); 0: four phase kernels
+                                      simulations per workgroup (at most 128 cars; default 64); 0: four phase kernels
                                       per tick.  Results are identical; no reference counterpart */
 };
 
