@@ -78,7 +78,7 @@ def measured_traffic(kernel: str, n_sim: int, n_cars: int, tick_skip: int, parts
     """HBM bytes per dispatch of `kernel` from the committed rocprofv3
     FETCH_SIZE / WRITE_SIZE summary of the headline workload (copy-calibrated);
     None for any other workload or when the summary is absent."""
-    if (n_sim, n_cars, tick_skip, parts, window) != (65536, 2, 8, 1, 128) or not TRAFFIC_FILE.is_file():
+    if (n_sim, n_cars, tick_skip, parts, window) != (65536, 2, 8, 1, 64) or not TRAFFIC_FILE.is_file():
         return None
     for line in TRAFFIC_FILE.read_text().splitlines():
         f = line.split()
