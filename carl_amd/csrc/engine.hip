@@ -15,6 +15,7 @@
 // kernel hands the car-arena kernel a small per-car workspace (wheel hits and
 // the deepest arena contact).
 #include <dlfcn.h>
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -735,33 +736,38 @@ void freeAll(carl_env* e)
     if (e->stream) (void)hipStreamDestroy(e->stream);
 }
 
-// Timing events of the current timed launch: begin before it, end after it,
-// both on the environment stream (events are created on first use).
-int markEvent(carl_env* e, size_t slot)
+// Timing events of the next timed launch: a start and an end event from a
+// reusable pool (created on first use), both null when timing is off.
+int timedPair(carl_env* e, int kernel, hipEvent_t* begin, hipEvent_t* end)
 {
-    while (e->marks.size() <= slot) {
+    *begin = *end = nullptr;
+    if (!e->timing) return CARL_OK;
+    const size_t slot = 2 * e->timedLaunches;
+    while (e->marks.size() < slot + 2) {
         hipEvent_t ev;
         HIP_TRY(hipEventCreate(&ev));
         e->marks.push_back(ev);
     }
-    HIP_TRY(hipEventRecord(e->marks[slot], e->stream));
+    if (e->markKernel.size() <= e->timedLaunches) e->markKernel.resize(e->timedLaunches + 1);
+    e->markKernel[e->timedLaunches++] = kernel;
+    *begin = e->marks[slot];
+    *end = e->marks[slot + 1];
     return CARL_OK;
 }
 
-int markBegin(carl_env* e, int kernel)
+// A tick kernel launch; when timed, its start and end events are recorded
+// by the dispatch itself (hipExtLaunchKernelGGL).
+template <typename... P, typename... A>
+int launchTick(carl_env* e, bool timed, int kernel, void (*k)(P...), dim3 grid, dim3 block, hipStream_t st,
+               A&&... args)
 {
-    if (!e->timing) return CARL_OK;
-    if (e->markKernel.size() <= e->timedLaunches) e->markKernel.resize(e->timedLaunches + 1);
-    e->markKernel[e->timedLaunches] = kernel;
-    return markEvent(e, 2 * e->timedLaunches);
-}
-
-int markEnd(carl_env* e)
-{
-    if (!e->timing) return CARL_OK;
-    const int rc = markEvent(e, 2 * e->timedLaunches + 1);
-    e->timedLaunches++;
-    return rc;
+    hipEvent_t b = nullptr, en = nullptr;
+    if (timed) {
+        const int rc = timedPair(e, kernel, &b, &en);
+        if (rc != CARL_OK) return rc;
+    }
+    hipExtLaunchKernelGGL(k, grid, block, 0, st, b, en, 0, static_cast<P>(args)...);
+    return CARL_OK;
 }
 
 #define CARL_MARK(expr)                   \
@@ -797,10 +803,9 @@ int launchTicks(carl_env* e, int kind, const void* actions, int n)
         for (int p = 0; p < parts; p++) {
             const SimRange r = range[p];
             const bool timed = p == 0;
-            if (timed) CARL_MARK(markBegin(e, CARL_KERNEL_WINDOW));
-            tickWindowKernel<<<e->grid(r.end - r.begin, wsb), kWindowBlock, 0, stream[p]>>>(
-                d, e->ws, e->contactScreen, kind, actions, e->tickCount + 1, n, wsb, r);
-            if (timed) CARL_MARK(markEnd(e));
+            CARL_MARK(launchTick(e, timed, CARL_KERNEL_WINDOW, tickWindowKernel, dim3(e->grid(r.end - r.begin, wsb)),
+                                 dim3(kWindowBlock), stream[p], d, e->ws, e->contactScreen, kind, actions,
+                                 e->tickCount + 1, n, wsb, r));
         }
     }
     for (int k = 0; e->windowSims == 0 && k < n; k++) {
@@ -810,18 +815,14 @@ int launchTicks(carl_env* e, int kind, const void* actions, int n)
             const int sims = r.end - r.begin, cars = sims * e->nCars;
             hipStream_t st = stream[p];
             const bool timed = p == 0;
-            if (timed) CARL_MARK(markBegin(e, CARL_KERNEL_CONTACT));
-            contactKernel<<<e->grid(cars, kContactOwners), kContactBlock, 0, st>>>(d, e->ws, e->contactScreen, r);
-            if (timed) CARL_MARK(markEnd(e));
-            if (timed) CARL_MARK(markBegin(e, CARL_KERNEL_CAR_ARENA));
-            carArenaKernel<<<e->grid(cars, kTickBlock), kTickBlock, 0, st>>>(d, e->ws, kind, actions, tick, r);
-            if (timed) CARL_MARK(markEnd(e));
-            if (timed) CARL_MARK(markBegin(e, CARL_KERNEL_BALL));
-            ballKernel<<<e->grid(sims, kBallOwners), kBallBlock, 0, st>>>(d, tick, r);
-            if (timed) CARL_MARK(markEnd(e));
-            if (timed) CARL_MARK(markBegin(e, CARL_KERNEL_FINISH));
-            finishKernel<<<e->grid(sims, spb), spb * e->nCars, 0, st>>>(d, spb, r);
-            if (timed) CARL_MARK(markEnd(e));
+            CARL_MARK(launchTick(e, timed, CARL_KERNEL_CONTACT, contactKernel, dim3(e->grid(cars, kContactOwners)),
+                                 dim3(kContactBlock), st, d, e->ws, e->contactScreen, r));
+            CARL_MARK(launchTick(e, timed, CARL_KERNEL_CAR_ARENA, carArenaKernel, dim3(e->grid(cars, kTickBlock)),
+                                 dim3(kTickBlock), st, d, e->ws, kind, actions, tick, r));
+            CARL_MARK(launchTick(e, timed, CARL_KERNEL_BALL, ballKernel, dim3(e->grid(sims, kBallOwners)),
+                                 dim3(kBallBlock), st, d, tick, r));
+            CARL_MARK(launchTick(e, timed, CARL_KERNEL_FINISH, finishKernel, dim3(e->grid(sims, spb)),
+                                 dim3(spb * e->nCars), st, d, spb, r));
         }
     }
     HIP_TRY(hipGetLastError());

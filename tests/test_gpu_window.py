@@ -72,3 +72,22 @@ def test_window_per_tick_steps_with_masked_resets(gpu):
 
 def test_window_single_car(gpu):
     _run_both(1000, 1, 0, 8, 15, workloads.random_reset_state, seed=46)
+
+
+def test_tick_timing_counts_every_launch(gpu):
+    """The HIP-event timing records one positive duration per tick-kernel launch of partition 0."""
+    n, frameskip, steps = 2048, 4, 3
+    env = carl_amd.Env(n, 1, 1, 3, frameskip, True, False, False)
+    actions = dev(workloads.random_continuous_actions(np.random.default_rng(5), n, 2))
+    phase = {name: steps * frameskip for name in ("contactKernel", "carArenaKernel", "ballKernel", "finishKernel")}
+    for window, streams, expect in ((64, 1, {"tickWindowKernel": steps}), (64, 3, {"tickWindowKernel": steps}),
+                                    (0, 1, phase)):
+        env.tick_window = window
+        env.tick_streams = streams
+        env.enable_tick_timing(True)
+        for _ in range(steps):
+            env.step_continuous(actions)
+        timing = env.tick_timing()
+        env.enable_tick_timing(False)
+        assert {k: v[1] for k, v in timing.items()} == expect, (window, streams, timing)
+        assert all(v[0] > 0.0 for v in timing.values()), timing
