@@ -16,6 +16,9 @@ Prints one JSON line:
                  the timed steps, against 8 TB/s
   tick_pipeline  the whole tick (four kernels) against the 1,488 B per 1v1
                  sim-tick floor: persistent state read + written + actions
+  packing        the step's packing kernel (packing_bytes x n_sim per
+                 launch) against 8 TB/s, timed the same way over up to 200
+                 further steps after the timed region
   cpu_baseline   the CPU model of the same physics (oracle/liboracle.so), one
                  1v1 arena per thread on this host's cores, direct controls
                  held 8 ticks (bounded sample)
@@ -69,6 +72,27 @@ def kernel_bytes(kernel: str, n_cars: int, ticks: int) -> int:
         "finishKernel": n_cars * (18 + 17) + 34 + 18,
     }[kernel]
     return 4 * words
+
+
+PACK_KERNEL = "stepEnvKernel"
+
+
+def packing_bytes(n_cars: int, obs_dim: int, state_dim: int) -> int:
+    """Algorithmic HBM bytes per simulation of one launch of the step's packing
+    kernel: every output written once, the state words its rows read once,
+    and the actions read and kept once (the transition observations of the
+    finished simulations depend on the data and are left out).
+      writes  observations n_cars*obs_dim, state and transition state
+              2*state_dim words; rewards, score differences and episode ticks
+              (current and transition) 4 B each, dones and overtime flags
+              1 B each (23 B); the kept actions 28 B per car
+      reads   per car 26 state words (pose, velocity, spin, boost and flag
+              words of the rows); per simulation 49 (ball 9, pad cooldowns
+              34, score, clock and touch words 6); the actions 28 B per car
+    """
+    writes = 4 * (n_cars * obs_dim + 2 * state_dim) + 23 + ACTION_BYTES * n_cars
+    reads = 4 * (26 * n_cars + 49) + ACTION_BYTES * n_cars
+    return writes + reads
 
 
 TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_1v1_n65536_ts8.md"
@@ -184,6 +208,12 @@ def main() -> None:
     seconds = time.perf_counter() - t0
     timing = env.tick_timing()        # {kernel: (total ms, launches)} over the timed steps
     env.enable_tick_timing(False)
+    # the packing kernel is timed over further steps, outside the timed region
+    env.enable_tick_timing(True, ticks=False, packing=True)
+    for i in range(args.steps, args.steps + min(args.steps, 200)):
+        reward = env_step(i)
+    timing.update(env.tick_timing())
+    env.enable_tick_timing(False)
     del reward
 
     sim_ticks = n_sim * args.tick_skip * args.steps
@@ -191,6 +221,7 @@ def main() -> None:
 
     # dominant kernel: the tick kernel with the largest share of the timed
     # region, timed on the engine stream by the engine's own events
+    pack_timing = timing.pop(PACK_KERNEL, None)
     kernel = max(timing, key=lambda k: timing[k][0])
     kernel_ms, launches = timing[kernel]
     launch_ms = kernel_ms / launches
@@ -248,6 +279,22 @@ def main() -> None:
             "achieved_GBs": tick_bytes(n_cars) * sim_ticks / (tick_ms * 1e-3) / 1e9,
         },
     }
+    if pack_timing:
+        pack_ms = pack_timing[0] / pack_timing[1]
+        state_dim = torch.from_dlpack(env.get_state()).shape[1]
+        pack_bytes = packing_bytes(n_cars, env.obs_dim, state_dim) * n_sim
+        pack_gbs = pack_bytes / (pack_ms * 1e-3) / 1e9
+        result["packing"] = {
+            "bound": "hbm",
+            "kernel": PACK_KERNEL,
+            "achieved": pack_gbs,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": pack_gbs / HBM_PEAK_GBS,
+            "launch_ms": pack_ms,
+            "launches": pack_timing[1],
+            "bytes_per_launch": pack_bytes,
+        }
     if args.cpu_ticks > 0:
         result["cpu_baseline"] = cpu_baseline(args.cpu_ticks, args.seed)
     print(json.dumps(result), flush=True)

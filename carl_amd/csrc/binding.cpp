@@ -481,7 +481,11 @@ public:
 
     void resetDones() { check(carl_env_reset_dones(env_)); }
     void synchronize() { check(carl_env_synchronize(env_)); }
-    void enableTiming(bool on) { check(carl_env_enable_timing(env_, on ? 1 : 0)); }
+    void enableTiming(bool on, bool ticks, bool packing)
+    {
+        const int flags = (ticks ? CARL_TIME_TICKS : 0) | (packing ? CARL_TIME_PACKING : 0);
+        check(carl_env_enable_timing(env_, on ? flags : 0));
+    }
     py::dict tickTiming()
     {
         double ms[CARL_TICK_KERNELS];
@@ -640,7 +644,8 @@ PYBIND11_MODULE(_carl, m)
         .def("tick", &Env::tick, py::arg("actions"), py::arg("kind"), py::arg("n_ticks") = 1)
         .def("reset_dones", &Env::resetDones)
         .def("synchronize", &Env::synchronize)
-        .def("enable_tick_timing", &Env::enableTiming, py::arg("enable") = true)
+        .def("enable_tick_timing", &Env::enableTiming, py::arg("enable") = true, py::arg("ticks") = true,
+             py::arg("packing") = false)
         .def("tick_timing", &Env::tickTiming)
         .def_property_readonly("tick_count", [](Env& e) { return e.param(CARL_PARAM_TICK_COUNT); });
 }

@@ -691,7 +691,7 @@ struct carl_env {
     hipStream_t aux[kMaxTickStreams - 1] = {};
     hipEvent_t fork = nullptr, join[kMaxTickStreams - 1] = {};
     int windowSims = kDefaultWindowSims;  // simulations per block of the tick-window kernel (0: phase kernels)
-    bool timing = false;
+    int timing = 0;                      // CARL_TIME_* flags
     // timing: per timed launch a start and an end event (reusable pool) and
     // the launch's kernel id
     size_t timedLaunches = 0;
@@ -741,7 +741,7 @@ void freeAll(carl_env* e)
 int timedPair(carl_env* e, int kernel, hipEvent_t* begin, hipEvent_t* end)
 {
     *begin = *end = nullptr;
-    if (!e->timing) return CARL_OK;
+    if (!(e->timing & (kernel == CARL_KERNEL_STEP_ENV ? CARL_TIME_PACKING : CARL_TIME_TICKS))) return CARL_OK;
     const size_t slot = 2 * e->timedLaunches;
     while (e->marks.size() < slot + 2) {
         hipEvent_t ev;
@@ -758,15 +758,15 @@ int timedPair(carl_env* e, int kernel, hipEvent_t* begin, hipEvent_t* end)
 // A tick kernel launch; when timed, its start and end events are recorded
 // by the dispatch itself (hipExtLaunchKernelGGL).
 template <typename... P, typename... A>
-int launchTick(carl_env* e, bool timed, int kernel, void (*k)(P...), dim3 grid, dim3 block, hipStream_t st,
-               A&&... args)
+int launchTick(carl_env* e, bool timed, int kernel, void (*k)(P...), dim3 grid, dim3 block, uint32_t lds,
+               hipStream_t st, A&&... args)
 {
     hipEvent_t b = nullptr, en = nullptr;
     if (timed) {
         const int rc = timedPair(e, kernel, &b, &en);
         if (rc != CARL_OK) return rc;
     }
-    hipExtLaunchKernelGGL(k, grid, block, 0, st, b, en, 0, static_cast<P>(args)...);
+    hipExtLaunchKernelGGL(k, grid, block, lds, st, b, en, 0, static_cast<P>(args)...);
     return CARL_OK;
 }
 
@@ -804,7 +804,7 @@ int launchTicks(carl_env* e, int kind, const void* actions, int n)
             const SimRange r = range[p];
             const bool timed = p == 0;
             CARL_MARK(launchTick(e, timed, CARL_KERNEL_WINDOW, tickWindowKernel, dim3(e->grid(r.end - r.begin, wsb)),
-                                 dim3(kWindowBlock), stream[p], d, e->ws, e->contactScreen, kind, actions,
+                                 dim3(kWindowBlock), 0, stream[p], d, e->ws, e->contactScreen, kind, actions,
                                  e->tickCount + 1, n, wsb, r));
         }
     }
@@ -816,13 +816,13 @@ int launchTicks(carl_env* e, int kind, const void* actions, int n)
             hipStream_t st = stream[p];
             const bool timed = p == 0;
             CARL_MARK(launchTick(e, timed, CARL_KERNEL_CONTACT, contactKernel, dim3(e->grid(cars, kContactOwners)),
-                                 dim3(kContactBlock), st, d, e->ws, e->contactScreen, r));
+                                 dim3(kContactBlock), 0, st, d, e->ws, e->contactScreen, r));
             CARL_MARK(launchTick(e, timed, CARL_KERNEL_CAR_ARENA, carArenaKernel, dim3(e->grid(cars, kTickBlock)),
-                                 dim3(kTickBlock), st, d, e->ws, kind, actions, tick, r));
+                                 dim3(kTickBlock), 0, st, d, e->ws, kind, actions, tick, r));
             CARL_MARK(launchTick(e, timed, CARL_KERNEL_BALL, ballKernel, dim3(e->grid(sims, kBallOwners)),
-                                 dim3(kBallBlock), st, d, tick, r));
+                                 dim3(kBallBlock), 0, st, d, tick, r));
             CARL_MARK(launchTick(e, timed, CARL_KERNEL_FINISH, finishKernel, dim3(e->grid(sims, spb)),
-                                 dim3(spb * e->nCars), st, d, spb, r));
+                                 dim3(spb * e->nCars), 0, st, d, spb, r));
         }
     }
     HIP_TRY(hipGetLastError());
@@ -1099,7 +1099,8 @@ int carl_env_step(carl_env* e, int kind, const void* actions)
     io.frameskip = e->frameskip; io.tickCount = e->tickCount; io.nOrange = e->nOrange;
     io.rule = e->rule();
     const size_t lds = std::max(packLdsBytes(e->obsDim), packLdsBytes(e->stateDim));
-    stepEnvKernel<<<e->grid(e->nSim, kStepSims), kPackBlock, lds, e->stream>>>(e->dev(), io);
+    CARL_TRY(launchTick(e, true, CARL_KERNEL_STEP_ENV, stepEnvKernel, dim3(e->grid(e->nSim, kStepSims)),
+                        dim3(kPackBlock), (uint32_t)lds, e->stream, e->dev(), io));
     HIP_TRY(hipGetLastError());
     return CARL_OK;
 }
@@ -1275,7 +1276,7 @@ int carl_env_enable_timing(carl_env* e, int enable)
 {
     CARL_TRY(checkEnv(e));
     HIP_TRY(hipStreamSynchronize(e->stream));
-    e->timing = enable != 0;
+    e->timing = enable & (CARL_TIME_TICKS | CARL_TIME_PACKING);
     e->timedLaunches = 0;
     return CARL_OK;
 }
@@ -1302,7 +1303,7 @@ int carl_env_tick_timing(carl_env* e, double* kernelMs, int* launches)
 const char* carl_tick_kernel_name(int kernel)
 {
     static const char* names[CARL_TICK_KERNELS] = { "contactKernel", "carArenaKernel", "ballKernel", "finishKernel",
-                                                    "tickWindowKernel" };
+                                                     "tickWindowKernel", "stepEnvKernel" };
     return kernel >= 0 && kernel < CARL_TICK_KERNELS ? names[kernel] : "";
 }
 

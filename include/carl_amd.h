@@ -303,11 +303,17 @@ enum {
     CARL_KERNEL_BALL = 2,       /* episode clock, car-car pairs, ball-arena, car-ball, goal */
     CARL_KERNEL_FINISH = 3,     /* integration, impulse caches, boost pads */
     CARL_KERNEL_WINDOW = 4,     /* all four phases of every tick of an env step, one launch */
-    CARL_TICK_KERNELS = 5
+    CARL_KERNEL_STEP_ENV = 5,   /* an env step's packing after its ticks (rewards/dones .. state) */
+    CARL_TICK_KERNELS = 6
 };
 
-/* With timing enabled, HIP events recorded on the environment stream bracket
- * every tick kernel.  carl_env_tick_timing synchronises that stream and
+/* Timing selection for carl_env_enable_timing (bit flags; 0 turns it off). */
+enum { CARL_TIME_TICKS = 1, CARL_TIME_PACKING = 2 };
+
+/* With timing enabled, HIP events recorded by the dispatch bracket every
+ * tick kernel of partition 0 (CARL_TIME_TICKS) and every packing kernel of
+ * carl_env_step (CARL_TIME_PACKING).
+ * carl_env_tick_timing synchronises the environment stream and
  * returns, per kernel (arrays of CARL_TICK_KERNELS), the summed duration in
  * ms and the launch count since timing was enabled or last read, then clears
  * them.  Enabling or disabling also clears them. */

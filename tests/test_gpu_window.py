@@ -75,19 +75,30 @@ def test_window_single_car(gpu):
 
 
 def test_tick_timing_counts_every_launch(gpu):
-    """The HIP-event timing records one positive duration per tick-kernel launch of partition 0."""
+    """The HIP-event timing records one positive duration per tick-kernel launch of partition 0 and per packing launch."""
     n, frameskip, steps = 2048, 4, 3
     env = carl_amd.Env(n, 1, 1, 3, frameskip, True, False, False)
     actions = dev(workloads.random_continuous_actions(np.random.default_rng(5), n, 2))
     phase = {name: steps * frameskip for name in ("contactKernel", "carArenaKernel", "ballKernel", "finishKernel")}
-    for window, streams, expect in ((64, 1, {"tickWindowKernel": steps}), (64, 3, {"tickWindowKernel": steps}),
-                                    (0, 1, phase)):
-        env.tick_window = window
+    phase["stepEnvKernel"] = steps
+    window = {"tickWindowKernel": steps, "stepEnvKernel": steps}
+    for window_sims, streams, expect in ((64, 1, window), (64, 3, window), (0, 1, phase)):
+        env.tick_window = window_sims
         env.tick_streams = streams
-        env.enable_tick_timing(True)
+        env.enable_tick_timing(True, packing=True)
         for _ in range(steps):
             env.step_continuous(actions)
         timing = env.tick_timing()
         env.enable_tick_timing(False)
-        assert {k: v[1] for k, v in timing.items()} == expect, (window, streams, timing)
+        assert {k: v[1] for k, v in timing.items()} == expect, (window_sims, streams, timing)
         assert all(v[0] > 0.0 for v in timing.values()), timing
+    # each selection alone
+    env.tick_window = 64
+    env.tick_streams = 1
+    for ticks, packing, expect in ((True, False, {"tickWindowKernel": steps}), (False, True, {"stepEnvKernel": steps})):
+        env.enable_tick_timing(True, ticks=ticks, packing=packing)
+        for _ in range(steps):
+            env.step_continuous(actions)
+        timing = env.tick_timing()
+        env.enable_tick_timing(False)
+        assert {k: v[1] for k, v in timing.items()} == expect, (ticks, packing, timing)
