@@ -152,3 +152,41 @@ def dense_geometry_reset_state(rng: np.random.Generator, n_rows: int, n_cars: in
         "car_demoed": np.zeros((n_rows, n_cars), dtype=np.bool_),
         "car_boost": f32(rng.uniform(0, 100, (n_rows, n_cars))),
     }
+
+
+# boost pad centres (x, y, z), big pads first: the standard soccar layout
+PAD_XYZ = np.array([
+    (-3584, 0, 73), (3584, 0, 73), (-3072, 4096, 73), (3072, 4096, 73), (-3072, -4096, 73), (3072, -4096, 73),
+    (0, -4240, 70), (-1792, -4184, 70), (1792, -4184, 70), (-940, -3308, 70), (940, -3308, 70), (0, -2816, 70),
+    (-3584, -2484, 70), (3584, -2484, 70), (-1788, -2300, 70), (1788, -2300, 70), (-2048, -1036, 70),
+    (0, -1024, 70), (2048, -1036, 70), (-1024, 0, 70), (1024, 0, 70), (-2048, 1036, 70), (0, 1024, 70),
+    (2048, 1036, 70), (-1788, 2300, 70), (1788, 2300, 70), (-3584, 2484, 70), (3584, 2484, 70), (0, 2816, 70),
+    (-940, 3308, 70), (940, 3308, 70), (-1792, 4184, 70), (1792, 4184, 70), (0, 4240, 70)], dtype=np.float64)
+
+
+def pad_reset_state(rng: np.random.Generator, n_rows: int, n_cars: int) -> dict[str, np.ndarray]:
+    """Reset inputs with every car parked on a boost pad (about a third of the
+    cars share the first car's pad, so the last car in order takes it), with
+    empty, partial or full boost and a few cars demoed: pickups, pad
+    cooldowns and the pad split across threads on every tick."""
+    pads = rng.integers(0, len(PAD_XYZ), (n_rows, n_cars))
+    share = rng.uniform(size=(n_rows, n_cars)) < 0.35
+    pads[:, 1:] = np.where(share[:, 1:], pads[:, :1], pads[:, 1:])
+    car_pos = PAD_XYZ[pads].copy()
+    car_pos[..., :2] += rng.uniform(-90, 90, (n_rows, n_cars, 2))
+    car_pos[..., 2] = 17.0
+    yaw = rng.uniform(-np.pi, np.pi, (n_rows, n_cars))
+    rot = np.stack([np.zeros_like(yaw), np.zeros_like(yaw), np.sin(yaw / 2), np.cos(yaw / 2)], axis=-1)
+    car_vel = np.concatenate([rng.uniform(-300, 300, (n_rows, n_cars, 2)), np.zeros((n_rows, n_cars, 1))], axis=-1)
+    boost = rng.choice(np.array([0.0, 12.0, 50.0, 99.5, 100.0]), size=(n_rows, n_cars))
+    ball_pos = np.stack([rng.uniform(-3000, 3000, n_rows), rng.uniform(-4000, 4000, n_rows),
+                         rng.uniform(100, 1500, n_rows)], axis=1)
+    f32 = lambda x: np.ascontiguousarray(x, dtype=np.float32)  # noqa: E731
+    return {
+        "ball_position": f32(ball_pos), "ball_velocity": f32(rng.normal(size=(n_rows, 3)) * 500.0),
+        "ball_angular_velocity": f32(rng.normal(size=(n_rows, 3))),
+        "car_position": f32(car_pos), "car_rotation": f32(rot), "car_velocity": f32(car_vel),
+        "car_angular_velocity": f32(np.zeros((n_rows, n_cars, 3))),
+        "car_demoed": rng.uniform(size=(n_rows, n_cars)) < 0.05,
+        "car_boost": f32(boost),
+    }

@@ -14,7 +14,7 @@ import pytest
 import torch
 
 from carl_amd import workloads
-from gpu_harness import Pair, dense_geometry_reset_state, dev, gpu_state
+from gpu_harness import Pair, dense_geometry_reset_state, dev, gpu_state, pad_reset_state
 
 pytestmark = pytest.mark.gpu
 
@@ -104,6 +104,23 @@ def test_clustered_3v3_contacts(gpu):
         p.step_continuous(workloads.random_continuous_actions(rng, n, 6))
         _assert_clean(p.state_mismatches(), f"state after step {step}")
         _assert_clean(p.output_mismatches(), f"outputs after step {step}")
+    p.close()
+
+
+@pytest.mark.parametrize("n_blue,n_orange", [(1, 1), (2, 2), (4, 4)])
+def test_boost_pad_pickups(gpu, n_blue, n_orange):
+    """Cars parked on boost pads, some sharing one (the last car in order
+    takes it), with empty to full boost: pickups and cooldowns against the
+    oracle, up to the largest team size."""
+    rng = np.random.default_rng(16 + n_blue)
+    n, nc = 64, n_blue + n_orange
+    p = Pair(n, n_blue, n_orange, seed=6, frameskip=2)
+    p.apply_reset_state(pad_reset_state(rng, n, nc))
+    _assert_clean(p.state_mismatches(), f"{n_blue}v{n_orange} state after pad reset")
+    for step in range(10):
+        p.step_continuous(workloads.random_continuous_actions(rng, n, nc))
+        _assert_clean(p.state_mismatches(), f"{n_blue}v{n_orange} state after step {step}")
+        _assert_clean(p.output_mismatches(), f"{n_blue}v{n_orange} outputs after step {step}")
     p.close()
 
 

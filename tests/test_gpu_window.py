@@ -13,7 +13,7 @@ import torch
 
 import carl_amd
 from carl_amd import workloads
-from gpu_harness import dense_geometry_reset_state, describe_mismatch, dev, gpu_state
+from gpu_harness import dense_geometry_reset_state, describe_mismatch, dev, gpu_state, pad_reset_state
 from abi import CAR_NAMES, SIM_NAMES
 
 pytestmark = pytest.mark.gpu
@@ -72,6 +72,14 @@ def test_window_per_tick_steps_with_masked_resets(gpu):
 
 def test_window_single_car(gpu):
     _run_both(1000, 1, 0, 8, 15, workloads.random_reset_state, seed=46)
+
+
+@pytest.mark.parametrize("n_blue,n_orange,window", [(1, 1, 64), (2, 2, 37), (4, 3, 18), (4, 4, 64)])
+def test_window_boost_pad_split_and_large_teams(gpu, n_blue, n_orange, window):
+    """Cars parked on pads (some sharing one): the window kernel splits each
+    simulation's pads over several threads, the phase kernels take them in one
+    thread; both must give the same boosts and cooldowns."""
+    _run_both(900, n_blue, n_orange, 2, 12, pad_reset_state, seed=47 + n_blue + n_orange, window=window)
 
 
 def test_tick_timing_counts_every_launch(gpu):
