@@ -61,3 +61,29 @@ def test_null_handles_are_value_errors(lib):
     assert lib.carl_env_reset(None) == err
     assert lib.carl_env_synchronize(None) == err
     assert "null environment handle" in lib.carl_last_error().decode()
+
+
+def test_boost_pad_cylinders_are_disjoint():
+    """The window kernel splits a simulation's boost pads over several threads,
+    which gives the serial result only if no car position can lie in two pads'
+    cylinders: every pair of pad circles in the engine's table is apart."""
+    import itertools
+    import re
+    from pathlib import Path
+
+    import numpy as np
+
+    text = (Path(__file__).resolve().parents[1] / "carl_amd" / "csrc" / "constants.h").read_text()
+    body = text[text.index("kPadPos[kPads][3] = {"):]
+    body = body[:body.index("};")]
+    pads = [tuple(float(v) for v in m) for m in re.findall(r"\{\s*(-?[\d.]+)f,\s*(-?[\d.]+)f,\s*(-?[\d.]+)f\s*\}", body)]
+    big = float(re.search(r"kBigPadRadius = ([\d.]+)f", text).group(1))
+    small = float(re.search(r"kSmallPadRadius = ([\d.]+)f", text).group(1))
+    n_big = 6  # big pads come first in the table
+    assert len(pads) == 34
+    radius = [big] * n_big + [small] * (len(pads) - n_big)
+    gaps = [np.hypot(pads[i][0] - pads[j][0], pads[i][1] - pads[j][1]) - radius[i] - radius[j]
+            for i, j in itertools.combinations(range(len(pads)), 2)]
+    assert min(gaps) > 0.0, min(gaps)
+    # the big pads are the six at |x| >= 3072 (corners and mid-field sides)
+    assert all(abs(p[0]) >= 3072 for p in pads[:n_big])
