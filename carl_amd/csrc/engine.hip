@@ -287,6 +287,11 @@ constexpr int kDefaultWindowSims = 64;
 #endif
 constexpr int kWindowContactDepth = CARL_WINDOW_CONTACT_DEPTH;
 
+// The waves' contact-search and ball-gather areas share one LDS block, and
+// one wave's ball area overlaps another wave's contact area (ball[1] lies
+// inside contact[0]).  Every phase change of the window kernel is therefore a
+// workgroup barrier: no wave may start a tick's contact search while another
+// is still in the previous tick's ball phase.
 union WindowLds {
     ContactLds contact[kWindowWaves];
     BallLds ball[kWindowWaves];
