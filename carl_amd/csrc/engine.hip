@@ -406,16 +406,40 @@ DI void packRowsParts(float* out, int rowLen, int r0, int r1, Keep&& keep, Part&
         const int rows = min(chunk, r1 - c0);
         const bool mine = lane < rows && keep(c0 + lane);
         if (q == 0) on[lane] = mine;
-        if (!__syncthreads_or(mine)) continue;
+        const int kept = __syncthreads_count(mine);   // every row counted by each of the kRowParts waves
+        if (kept == 0) continue;
         if (mine) part(c0 + lane, q, packLds + lane * stride);
         __syncthreads();
         float* dst = out + (size_t)c0 * rowLen;
-        int rr = t / rowLen, c = t % rowLen;
-        for (int e = t; e < rows * rowLen; e += kPackBlock) {
-            if (on[rr]) dst[e] = packLds[rr * stride + c];
-            rr += rowStep;
-            c += colStep;
-            if (c >= rowLen) { c -= rowLen; rr++; }
+        const int total = rows * rowLen;
+        if (kept == kRowParts * rows && ((size_t)dst & 15) == 0) {
+            // every row kept: the chunk is one contiguous run, stored 16 bytes
+            // per lane and instruction
+            const int step = 4 * kPackBlock, rs = step / rowLen, cs = step % rowLen;
+            int rr = 4 * t / rowLen, c = 4 * t % rowLen;
+            for (int e = 4 * t; e + 3 < total; e += step) {
+                float v[4];
+                int r2 = rr, c2 = c;
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    v[k] = packLds[r2 * stride + c2];
+                    if (++c2 == rowLen) { c2 = 0; r2++; }
+                }
+                *reinterpret_cast<float4*>(dst + e) = make_float4(v[0], v[1], v[2], v[3]);
+                rr += rs;
+                c += cs;
+                if (c >= rowLen) { c -= rowLen; rr++; }
+            }
+            const int e = (total & ~3) + t;
+            if (e < total) dst[e] = packLds[(e / rowLen) * stride + e % rowLen];
+        } else {
+            int rr = t / rowLen, c = t % rowLen;
+            for (int e = t; e < total; e += kPackBlock) {
+                if (on[rr]) dst[e] = packLds[rr * stride + c];
+                rr += rowStep;
+                c += colStep;
+                if (c >= rowLen) { c -= rowLen; rr++; }
+            }
         }
         __syncthreads();
     }
