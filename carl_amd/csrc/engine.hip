@@ -487,6 +487,7 @@ struct StepIO {
 __global__ __launch_bounds__(kPackBlock) void stepEnvKernel(Dev d, StepIO io)
 {
     __shared__ int done[kStepSims];
+    __shared__ int fate[kStepSims];   // DoneOutcome of each simulation
     const int t = threadIdx.x, nC = d.nCars;
     const int s0 = blockIdx.x * kStepSims, s1 = min(s0 + kStepSims, d.nSim);
     const int s = s0 + t;
@@ -494,14 +495,23 @@ __global__ __launch_bounds__(kPackBlock) void stepEnvKernel(Dev d, StepIO io)
         const size_t w0 = (size_t)s0 * nC * 7;
         for (int w = t; w < (s1 - s0) * nC * 7; w += kPackBlock) io.actionCopy[w0 + w] = io.actions[w0 + w];
     }
+    // rewards, dones and the transition match state; each simulation's
+    // reset outcome, and with it the match state after the resets, follows
+    // from the same words
     if (s < s1) {
-        const bool dn = simDone(d, s, io.tickCount, io.rule);
-        io.rewards[s] = (float)d.si(CARL_SIM_LAST_SCORER, s);
+        const MatchWords m = matchWords(d, s);
+        const bool dn = simDoneFrom(m, io.tickCount, io.rule);
+        const int outcome = doneOutcome(m, io.tickCount, io.rule);
+        io.rewards[s] = (float)m.scorer;
         io.dones[s] = dn;
-        io.tscore[s] = d.si(CARL_SIM_BLUE_SCORE, s) - d.si(CARL_SIM_ORANGE_SCORE, s);
-        io.tticks[s] = d.si(CARL_SIM_EPISODE_TICKS, s);
-        io.tovertime[s] = d.si(CARL_SIM_OVERTIME, s) != 0;
+        io.tscore[s] = m.blue - m.orange;
+        io.tticks[s] = m.ep;
+        io.tovertime[s] = m.overtime != 0;
+        io.score[s] = outcome == kReset ? 0 : m.blue - m.orange;
+        io.ticks[s] = outcome == kReset ? 0 : m.ep;
+        io.overtime[s] = outcome == kReset ? false : (outcome == kOvertimeEntered || m.overtime != 0);
         done[t] = dn;
+        fate[t] = outcome;
     }
     __syncthreads();
     packRowsParts(
@@ -512,13 +522,8 @@ __global__ __launch_bounds__(kPackBlock) void stepEnvKernel(Dev d, StepIO io)
         [&](int a, int q, float* o) {
             packObservationPart(d, a / nC, a % nC, io.invert != 0, io.normalize != 0, io.prev != 0, q, o);
         });
-    if (s < s1) resetAfterDone(d, s, io.tickCount, io.rule, io.nOrange);
+    if (s < s1) applyDoneOutcome(d, s, fate[t], io.tickCount, io.nOrange);
     __syncthreads();
-    if (s < s1) {
-        io.score[s] = d.si(CARL_SIM_BLUE_SCORE, s) - d.si(CARL_SIM_ORANGE_SCORE, s);
-        io.ticks[s] = d.si(CARL_SIM_EPISODE_TICKS, s);
-        io.overtime[s] = d.si(CARL_SIM_OVERTIME, s) != 0;
-    }
     packRowsParts(
         io.obs, io.obsDim, s0 * nC, s1 * nC, [](int) { return true; },
         [&](int a, int q, float* o) {

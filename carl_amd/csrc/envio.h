@@ -174,16 +174,30 @@ struct DoneRule {
     int maxTicks, overtimeTicks, noTouchTicks;
 };
 
+// The match words that decide whether an episode ends.
+struct MatchWords {
+    int ep, blue, orange, overtime, scorer, lastTouch;
+};
+
+DI MatchWords matchWords(const Dev& d, int s)
+{
+    return MatchWords{ d.si(CARL_SIM_EPISODE_TICKS, s), d.si(CARL_SIM_BLUE_SCORE, s), d.si(CARL_SIM_ORANGE_SCORE, s),
+                       d.si(CARL_SIM_OVERTIME, s),      d.si(CARL_SIM_LAST_SCORER, s), d.si(CARL_SIM_LAST_TOUCH_TICK, s) };
+}
+
+DI bool simDoneFrom(const MatchWords& m, int tickCount, DoneRule rule)
+{
+    const bool overtime = m.overtime != 0;
+    const bool regExpired = m.ep >= rule.maxTicks && m.blue != m.orange;
+    const bool otExpired = overtime && m.ep >= rule.maxTicks + rule.overtimeTicks;
+    const bool scored = m.scorer != 0;
+    const bool timeout = rule.noTouchTicks > 0 && tickCount - m.lastTouch >= rule.noTouchTicks;
+    return (!overtime && regExpired) || otExpired || timeout || scored;
+}
+
 DI bool simDone(const Dev& d, int s, int tickCount, DoneRule rule)
 {
-    const int ep = d.si(CARL_SIM_EPISODE_TICKS, s);
-    const int blue = d.si(CARL_SIM_BLUE_SCORE, s), orange = d.si(CARL_SIM_ORANGE_SCORE, s);
-    const bool overtime = d.si(CARL_SIM_OVERTIME, s) != 0;
-    const bool regExpired = ep >= rule.maxTicks && blue != orange;
-    const bool otExpired = overtime && ep >= rule.maxTicks + rule.overtimeTicks;
-    const bool scored = d.si(CARL_SIM_LAST_SCORER, s) != 0;
-    const bool timeout = rule.noTouchTicks > 0 && tickCount - d.si(CARL_SIM_LAST_TOUCH_TICK, s) >= rule.noTouchTicks;
-    return (!overtime && regExpired) || otExpired || timeout || scored;
+    return simDoneFrom(matchWords(d, s), tickCount, rule);
 }
 
 // ------------------------------------------------------------------ resets
@@ -268,20 +282,29 @@ DI void fullResetSim(const Dev& d, int s, int nOrange)
     kickoffSim(d, s, 0, nOrange);
 }
 
-DI void resetAfterDone(const Dev& d, int s, int tickCount, DoneRule rule, int nOrange)
+// What the end-of-step reset does to one simulation: nothing, enter
+// overtime (a tie at the end of regulation), or reset it to a kickoff.
+enum DoneOutcome { kKept = 0, kOvertimeEntered = 1, kReset = 2 };
+
+DI int doneOutcome(const MatchWords& m, int tickCount, DoneRule rule)
 {
-    const bool scored = d.si(CARL_SIM_LAST_SCORER, s) != 0;
-    const int ep = d.si(CARL_SIM_EPISODE_TICKS, s);
-    const bool overtime = d.si(CARL_SIM_OVERTIME, s) != 0;
-    const bool noTouch = rule.noTouchTicks > 0 && tickCount - d.si(CARL_SIM_LAST_TOUCH_TICK, s) >= rule.noTouchTicks;
-    const bool otExpired = overtime && ep >= rule.maxTicks + rule.overtimeTicks;
-    const bool timeout = ep >= rule.maxTicks;
-    if (!overtime && !scored && !noTouch && ep >= rule.maxTicks
-        && d.si(CARL_SIM_BLUE_SCORE, s) == d.si(CARL_SIM_ORANGE_SCORE, s)) {
+    const bool scored = m.scorer != 0;
+    const bool overtime = m.overtime != 0;
+    const bool noTouch = rule.noTouchTicks > 0 && tickCount - m.lastTouch >= rule.noTouchTicks;
+    const bool otExpired = overtime && m.ep >= rule.maxTicks + rule.overtimeTicks;
+    const bool timeout = m.ep >= rule.maxTicks;
+    if (!overtime && !scored && !noTouch && m.ep >= rule.maxTicks && m.blue == m.orange) return kOvertimeEntered;
+    if (!(scored || noTouch || otExpired || (!overtime && timeout))) return kKept;
+    return kReset;
+}
+
+DI void applyDoneOutcome(const Dev& d, int s, int outcome, int tickCount, int nOrange)
+{
+    if (outcome == kOvertimeEntered) {
         d.sseti(CARL_SIM_OVERTIME, s, 1);
         return;
     }
-    if (!(scored || noTouch || otExpired || (!overtime && timeout))) return;
+    if (outcome != kReset) return;
     for (int f = CARL_SIM_BLUE_SCORE; f <= CARL_SIM_OVERTIME; f++) d.sseti(f, s, 0);
     kickoffSim(d, s, tickCount, nOrange);
     d.sseti(CARL_SIM_EPISODE_TICKS, s, 0);
@@ -297,6 +320,11 @@ DI void resetAfterDone(const Dev& d, int s, int tickCount, DoneRule rule, int nO
         }
     }
     for (int p = 0; p < kPads; p++) d.ssetf(CARL_SIM_PAD_COOLDOWN + p, s, 0.f);
+}
+
+DI void resetAfterDone(const Dev& d, int s, int tickCount, DoneRule rule, int nOrange)
+{
+    applyDoneOutcome(d, s, doneOutcome(matchWords(d, s), tickCount, rule), tickCount, nOrange);
 }
 
 // ----------------------------------------------------------------- setters
