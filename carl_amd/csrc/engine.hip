@@ -324,7 +324,7 @@ __global__ __launch_bounds__(kWindowBlock, 2) void tickWindowKernel(Dev d, uint3
         {
             // boost pads: the workgroup's threads split into kWindowBlock /
             // simsPerBlock parts, each taking a contiguous range of every
-            // simulation's pads (in 1v1 two parts of two waves each).  The
+            // simulation's pads (in 1v1 two parts, one wave each).  The
             // split is derived here from a copy of the thread index that the
             // optimiser cannot hoist, so it holds no registers through the
             // other phases.
