@@ -107,6 +107,27 @@ def test_clustered_3v3_contacts(gpu):
     p.close()
 
 
+@pytest.mark.parametrize("n_blue,frameskip", [(1, 8), (2, 1)])
+def test_short_episodes_timeouts_overtime_and_resets(gpu, n_blue, frameskip):
+    """Episodes of a few steps: regulation timeouts, ties that enter overtime,
+    overtime expiry and no-touch timeouts end simulations on most steps, so
+    the packing's reset decisions, the match state after the resets and the
+    transition rows of finished simulations all run against the oracle."""
+    rng = np.random.default_rng(18 + n_blue)
+    n, nc = 96, 2 * n_blue
+    p = Pair(n, n_blue, n_blue, seed=12, frameskip=frameskip)
+    p.set_param("max_ticks", 3 * frameskip + 1)
+    p.set_param("overtime_timeout_ticks", 2 * frameskip)
+    p.set_param("no_touch_timeout_ticks", 7 * frameskip)
+    half = np.arange(0, n, 2)
+    p.apply_reset_state(workloads.random_reset_state(rng, len(half), nc), simulation_indices=half.astype(np.int64))
+    for step in range(18):
+        p.step_continuous(workloads.random_continuous_actions(rng, n, nc))
+        _assert_clean(p.state_mismatches(), f"{n_blue}v{n_blue} state after step {step}")
+        _assert_clean(p.output_mismatches(), f"{n_blue}v{n_blue} outputs after step {step}")
+    p.close()
+
+
 @pytest.mark.parametrize("n_blue,n_orange", [(1, 1), (2, 2), (4, 4)])
 def test_boost_pad_pickups(gpu, n_blue, n_orange):
     """Cars parked on boost pads, some sharing one (the last car in order
