@@ -642,6 +642,8 @@ PYBIND11_MODULE(_carl, m)
         .def("export_state", &Env::exportState)
         .def("import_state", &Env::importState, py::arg("car_state"), py::arg("sim_state"), py::arg("tick_count"))
         .def("tick", &Env::tick, py::arg("actions"), py::arg("kind"), py::arg("n_ticks") = 1)
+        .def("get_actions", [](Env& e) { return e.buffer(CARL_BUF_ACTIONS); })
+        .def("get_continuous_actions", [](Env& e) { return e.buffer(CARL_BUF_CONTINUOUS_ACTIONS); })
         .def("reset_dones", &Env::resetDones)
         .def("synchronize", &Env::synchronize)
         .def("enable_tick_timing", &Env::enableTiming, py::arg("enable") = true, py::arg("ticks") = true,

@@ -15,7 +15,7 @@ from oracle_py import OracleEnv
 
 OUTPUTS = ("obs", "transition_obs", "state", "transition_state", "rewards", "dones", "score_difference",
            "episode_ticks", "transition_score_difference", "transition_episode_ticks", "overtime",
-           "transition_overtime")
+           "transition_overtime", "actions", "continuous_actions")
 
 
 def dev(x: np.ndarray) -> torch.Tensor:
@@ -78,6 +78,13 @@ class Pair:
     def step_discrete(self, actions: np.ndarray):
         self.gpu.step(dev(actions.astype(np.int32)))
         self.cpu.step(np.ascontiguousarray(actions, dtype=np.int32))
+
+    def tick(self, actions: np.ndarray, kind: int, n_ticks: int = 1):
+        """Bare physics ticks (no packing) on the same actions for both sides;
+        kind 2 takes a structured array of direct controls."""
+        words = np.ascontiguousarray(actions).view(np.int32 if kind != 1 else np.float32)
+        self.gpu.tick(dev(words.reshape(-1)), kind, n_ticks)
+        self.cpu.tick(np.ascontiguousarray(actions), kind, n_ticks)
 
     def apply_reset_state(self, values: dict, **kw):
         gv = {k: dev(v) for k, v in values.items()}

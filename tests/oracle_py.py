@@ -82,6 +82,7 @@ BUFFERS = {
     "dones": (6, np.bool_), "score_difference": (7, np.int32), "episode_ticks": (8, np.int32),
     "transition_score_difference": (9, np.int32), "transition_episode_ticks": (10, np.int32),
     "overtime": (11, np.bool_), "transition_overtime": (12, np.bool_),
+    "continuous_actions": (13, np.float32),
 }
 CAR_FIELDS = 81
 SIM_FIELDS = 67
@@ -206,6 +207,8 @@ class OracleEnv:
             return out.reshape(self.n_sim, self.n_cars, -1)
         if name in ("state", "transition_state"):
             return out.reshape(self.n_sim, -1)
+        if name in ("actions", "continuous_actions"):
+            return out.reshape(self.n_sim, self.n_cars, 7)
         return out
 
     def export_state(self):
