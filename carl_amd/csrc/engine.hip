@@ -21,6 +21,7 @@
 #include <algorithm>
 #include <array>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -659,7 +660,17 @@ __global__ void scanAddKernel(int32_t* out, int n, const int32_t* offsets)
     }
 }
 
-int runScan(const int32_t* in, int32_t* out, int n, hipStream_t stream)
+// 32-bit words of tile sums and their scan that runScanInto needs for n items
+// (every level of the recursion; 0 when one tile holds them all).
+size_t scanWorkWords(int n)
+{
+    const int tiles = (n + kScanTile - 1) / kScanTile;
+    return tiles <= 1 ? 0 : 2 * (size_t)tiles + scanWorkWords(tiles);
+}
+
+// Scan with the tile sums of every level in `work` (scanWorkWords(n) words
+// of device memory); every word of it is written before it is read.
+int runScanInto(const int32_t* in, int32_t* out, int n, hipStream_t stream, int32_t* work)
 {
     if (n <= 0) return CARL_OK;
     const int tiles = (n + kScanTile - 1) / kScanTile;
@@ -668,15 +679,58 @@ int runScan(const int32_t* in, int32_t* out, int n, hipStream_t stream)
         HIP_TRY(hipGetLastError());
         return CARL_OK;
     }
-    int32_t* sums = nullptr;
-    HIP_TRY(hipMallocAsync((void**)&sums, sizeof(int32_t) * 2 * tiles, stream));
+    int32_t* sums = work;
+    int32_t* offsets = work + tiles;
     scanTileKernel<<<tiles, kScanBlock, 0, stream>>>(in, out, n, sums);
     HIP_TRY(hipGetLastError());
-    const int rc = runScan(sums, sums + tiles, tiles, stream);
+    const int rc = runScanInto(sums, offsets, tiles, stream, work + 2 * (size_t)tiles);
     if (rc != CARL_OK) return rc;
-    scanAddKernel<<<tiles, kScanBlock, 0, stream>>>(out, n, sums + tiles);
+    scanAddKernel<<<tiles, kScanBlock, 0, stream>>>(out, n, offsets);
     HIP_TRY(hipGetLastError());
-    HIP_TRY(hipFreeAsync(sums, stream));
+    return CARL_OK;
+}
+
+int runScan(const int32_t* in, int32_t* out, int n, hipStream_t stream)
+{
+    const size_t words = scanWorkWords(n);
+    if (words == 0) return runScanInto(in, out, n, stream, nullptr);
+    int32_t* work = nullptr;
+    HIP_TRY(hipMallocAsync((void**)&work, sizeof(int32_t) * words, stream));
+    const int rc = runScanInto(in, out, n, stream, work);
+    const hipError_t freed = hipFreeAsync(work, stream);
+    if (rc != CARL_OK) return rc;
+    HIP_TRY(freed);
+    return CARL_OK;
+}
+
+// ---- the scan's tile sums in a fixed device array, for callers that cannot
+// allocate.  One copy per GPU; every call on a GPU shares it.
+constexpr int kScanNoAllocMaxItems = 1 << 26;
+constexpr size_t kScanScratchWords = 2 * (kScanNoAllocMaxItems / kScanTile) + 2 * 16;
+static_assert(kScanNoAllocMaxItems % kScanTile == 0, "whole tiles at the maximum");
+static_assert((kScanNoAllocMaxItems / kScanTile) <= 16 * kScanTile, "two sum levels cover the maximum");
+
+static __device__ __align__(256) int32_t scratch[kScanScratchWords];
+
+constexpr int kMaxDevices = 64;
+std::mutex scratchMutex;
+int32_t* scratchAddress[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device, looked up once per
+// device (the host-side name is not a device address).
+int scratchOnCurrentDevice(int32_t** out)
+{
+    int device = 0;
+    HIP_TRY(hipGetDevice(&device));
+    if (device < 0 || device >= kMaxDevices) return fail(CARL_ERR_RUNTIME, "device ordinal out of range");
+    std::lock_guard<std::mutex> lock(scratchMutex);
+    if (!scratchAddress[device]) {
+        void* ptr = nullptr;
+        HIP_TRY(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+        if (!ptr) return fail(CARL_ERR_RUNTIME, "scan scratch has no device address");
+        scratchAddress[device] = (int32_t*)ptr;
+    }
+    *out = scratchAddress[device];
     return CARL_OK;
 }
 
@@ -1367,6 +1421,20 @@ int carl_exclusive_scan_i32(const int32_t* in, int32_t* out, int n, void* stream
     if (n < 0) return fail(CARL_ERR_VALUE, "negative length");
     if (n > 0 && (!in || !out)) return fail(CARL_ERR_VALUE, "null scan buffer");
     return runScan(in, out, n, (hipStream_t)stream);
+}
+
+int carl_exclusive_scan_i32_noalloc(const int32_t* in, int32_t* out, int n, void* stream)
+{
+    if (n < 0) return fail(CARL_ERR_VALUE, "negative length");
+    if (n > kScanNoAllocMaxItems)
+        return fail(CARL_ERR_VALUE, "scan length exceeds the no-allocation maximum of "
+                                        + std::to_string(kScanNoAllocMaxItems) + " items");
+    if (n > 0 && (!in || !out)) return fail(CARL_ERR_VALUE, "null scan buffer");
+    if (n == 0) return CARL_OK;
+    int32_t* work = nullptr;
+    CARL_TRY(scratchOnCurrentDevice(&work));
+    if (scanWorkWords(n) > kScanScratchWords) return fail(CARL_ERR_VALUE, "scan scratch too small");
+    return runScanInto(in, out, n, (hipStream_t)stream, work);
 }
 
 }  // extern "C"

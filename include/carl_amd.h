@@ -327,6 +327,17 @@ const char* carl_tick_kernel_name(int kernel);
  * allowed).  Wave64 DPP/ballot scan, no library calls. */
 int carl_exclusive_scan_i32(const int32_t* in, int32_t* out, int n, void* stream);
 
+/* carl_exclusive_scan_i32 without any allocation: no counterpart in the
+ * reference.  For callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * tile sums live in a fixed device array of 65,568 words (256 KiB) held by
+ * each GPU the library runs on until the process ends; n may be at most
+ * 67,108,864 (2^26), larger n returns CARL_ERR_VALUE.  The array belongs to
+ * the device current at the call and is shared by every call on that GPU:
+ * calls that overlap on one GPU (other streams, other threads) race.  Same
+ * results as carl_exclusive_scan_i32. */
+int carl_exclusive_scan_i32_noalloc(const int32_t* in, int32_t* out, int n, void* stream);
+
 /* Message of the last failed call on this thread ("" if none). */
 const char* carl_last_error(void);
 
