@@ -98,17 +98,105 @@ def packing_bytes(n_cars: int, obs_dim: int, state_dim: int) -> int:
 TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_1v1_n65536_ts8.md"
 
 
-def measured_traffic(kernel: str, n_sim: int, n_cars: int, tick_skip: int, parts: int, window: int):
+def measured_traffic(kernel: str, n_sim: int, n_cars: int, tick_skip: int, parts: int, window: int,
+                     steps: int, warmup: int, tag: str = "traffic"):
     """HBM bytes per dispatch of `kernel` from the committed rocprofv3
-    FETCH_SIZE / WRITE_SIZE summary of the headline workload (copy-calibrated);
-    None for any other workload or when the summary is absent."""
+    FETCH_SIZE / WRITE_SIZE summary of the headline workload (copy-calibrated),
+    for the same window of steps (`steps` timed after `warmup`; tag
+    "traffic-after" for the `steps` steps after them, over which the packing
+    kernel is timed); None for any other workload or window, or when the
+    summary is absent."""
     if (n_sim, n_cars, tick_skip, parts, window) != (65536, 2, 8, 1, 64) or not TRAFFIC_FILE.is_file():
         return None
     for line in TRAFFIC_FILE.read_text().splitlines():
         f = line.split()
-        if len(f) == 3 and f[0] == "traffic" and f[1] == kernel:
-            return int(f[2])
+        if len(f) == 5 and f[0] == tag and f[1] == kernel and (int(f[2]), int(f[3])) == (steps, warmup):
+            return int(f[4])
     return None
+
+
+def _read_csv(path: Path) -> list[dict]:
+    import csv
+
+    with open(path, newline="") as fh:
+        return list(csv.DictReader(fh))
+
+
+def summarize_rocprof(trace_dir: str | None, fetch_dir: str | None, write_dir: str | None,
+                      copy_fetch_dir: str | None, copy_write_dir: str | None, copy_mib: int,
+                      steps: int, warmup: int) -> None:
+    """Markdown summary of rocprofv3 output of one bench run: per kernel, the
+    average dispatch duration over all dispatches and over the timed window
+    (dispatches warmup .. warmup+steps-1 of that kernel, in dispatch order;
+    for the packing kernel also the `steps` dispatches after it, over which
+    the bench times it), and the copy-calibrated FETCH_SIZE / WRITE_SIZE
+    bytes per dispatch over the same windows."""
+    def short(name: str) -> str:
+        # "(anonymous namespace)::tickWindowKernel(carl::Dev, ...)" -> "tickWindowKernel"
+        head = name.replace("(anonymous namespace)::", "")
+        return head.split("(")[0].split("<")[0].split()[-1] if "(" in head else head
+
+    def kernel_series(rows, value):
+        out: dict[str, list] = {}
+        for r in sorted(rows, key=lambda r: int(r["Dispatch_Id"])):
+            out.setdefault(short(r["Kernel_Name"]), []).append(value(r))
+        return out
+
+    def mean(xs):
+        return sum(xs) / len(xs) if xs else float("nan")
+
+    windows = {"timed": (warmup, warmup + steps), "after": (warmup + steps, warmup + 2 * steps)}
+    if trace_dir:
+        rows = _read_csv(next(Path(trace_dir).rglob("*kernel_trace.csv")))
+        dur = kernel_series(rows, lambda r: (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+        print("| kernel | dispatches | avg us (all) | avg us (timed steps) | avg us (steps after) |")
+        print("|---|---|---|---|---|")
+        for k, xs in sorted(dur.items(), key=lambda kv: -sum(kv[1])):
+            w = {n: mean(xs[a:b]) for n, (a, b) in windows.items()}
+            print(f"| {k} | {len(xs)} | {mean(xs):.1f} | {w['timed']:.1f} | {w['after']:.1f} |")
+        print()
+
+    def counter(dir_, name):
+        rows = [r for r in _read_csv(next(Path(dir_).rglob("*counter_collection.csv"))) if r["Counter_Name"] == name]
+        return kernel_series(rows, lambda r: float(r["Counter_Value"]))
+
+    if fetch_dir and write_dir and copy_fetch_dir and copy_write_dir:
+        copy_bytes = copy_mib * (1 << 20)
+        cf = max(mean(v) for v in counter(copy_fetch_dir, "FETCH_SIZE").values())
+        cw = max(mean(v) for v in counter(copy_write_dir, "WRITE_SIZE").values())
+        f_scale, w_scale = copy_bytes / (cf * 1024), copy_bytes / (cw * 1024)
+        print(f"Calibration: a {copy_mib} MiB device copy reads FETCH_SIZE {cf:.1f} KiB and WRITE_SIZE {cw:.1f} KiB: "
+              f"FETCH_SIZE x {f_scale:.3f}, WRITE_SIZE x {w_scale:.3f} to bytes.")
+        print()
+        fetch, write = counter(fetch_dir, "FETCH_SIZE"), counter(write_dir, "WRITE_SIZE")
+        print("| kernel | window | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | HBM bytes (scaled) |")
+        print("|---|---|---|---|---|---|")
+        lines = []
+        for k in sorted(fetch, key=lambda k: -sum(fetch[k])):
+            for n, (a, b) in windows.items():
+                fk, wk = fetch[k][a:b], write.get(k, [])[a:b]
+                if not fk or not wk:
+                    continue
+                total = mean(fk) * 1024 * f_scale + mean(wk) * 1024 * w_scale
+                print(f"| {k} | {n} | {len(fk)} | {mean(fk):.1f} | {mean(wk):.1f} | {total / 1e6:.1f} MB |")
+                if k in ("tickWindowKernel", PACK_KERNEL):
+                    tag = "traffic" if n == "timed" else "traffic-after"
+                    lines.append(f"{tag} {k} {steps} {warmup} {int(total)}")
+        print()
+        print("Machine-readable (read by bench.py for `roofline.traffic` and `packing.traffic`):")
+        print()
+        for line in lines:
+            print(line)
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def cpu_baseline(ticks_per_thread: int, seed: int) -> dict:
@@ -125,6 +213,9 @@ def cpu_baseline(ticks_per_thread: int, seed: int) -> dict:
         "value": rate,
         "unit": "sim-ticks/s",
         "cores": cores,
+        "per_core": rate / cores,
+        "cpu_model": cpu_model(),
+        "logical_cpus": os.cpu_count(),
         "kind": "port",
         "sample": (f"1v1 arena per thread x {cores} threads, {ticks_per_thread} ticks each, seeded direct "
                    f"controls held 8 ticks, done-resets every tick (CPU model of the same physics)"),
@@ -150,7 +241,16 @@ def main() -> None:
                          "(-1: engine default)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (HBM counter calibration) and exit")
+    ap.add_argument("--summarize-rocprof", nargs=5, metavar=("TRACE", "FETCH", "WRITE", "COPY_FETCH", "COPY_WRITE"),
+                    help="print a markdown summary of rocprofv3 output directories of one bench run "
+                         "(use - for an absent one; --steps/--warmup name its window, --copy-mib the copy size)")
+    ap.add_argument("--copy-mib", type=int, default=512)
     args = ap.parse_args()
+
+    if args.summarize_rocprof:
+        dirs = [None if d == "-" else d for d in args.summarize_rocprof]
+        summarize_rocprof(*dirs, args.copy_mib, args.steps, args.warmup)
+        return
 
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
@@ -257,6 +357,7 @@ def main() -> None:
             "parallelism": "single GPU",
             "tick_streams": parts,
             "tick_window": env.tick_window,
+            "timed_steps": f"env steps {args.warmup + 1}..{args.warmup + args.steps} after the initial reset",
         },
         "roofline": {
             "bound": "hbm",
@@ -265,7 +366,8 @@ def main() -> None:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": measured_traffic(kernel, n_sim, n_cars, args.tick_skip, parts, env.tick_window),
+            "traffic": measured_traffic(kernel, n_sim, n_cars, args.tick_skip, parts, env.tick_window,
+                                        args.steps, args.warmup),
             "traffic_source": TRAFFIC_FILE.name,
             "launch_ms": launch_ms,
             "launches": launches,
@@ -294,6 +396,9 @@ def main() -> None:
             "launch_ms": pack_ms,
             "launches": pack_timing[1],
             "bytes_per_launch": pack_bytes,
+            "traffic": measured_traffic(PACK_KERNEL, n_sim, n_cars, args.tick_skip, parts, env.tick_window,
+                                        args.steps, args.warmup, tag="traffic-after")
+            if args.steps <= 200 else None,
         }
     if args.cpu_ticks > 0:
         result["cpu_baseline"] = cpu_baseline(args.cpu_ticks, args.seed)
