@@ -54,13 +54,29 @@ int fail(int code, const std::string& msg)
 constexpr int kTickBlock = 256;
 constexpr int kMaxTickStreams = 4;
 
-// Per-tick car workspace between the contact and the car-arena kernels, one
-// plane of nTotal 32-bit words each: wheel hit distance, normal xyz and
-// source per wheel, then the cell reference of the deepest arena contact.
+// Per-tick car workspace between the contact and the car-arena kernels, 31
+// 32-bit words per car: wheel hit distance, normal xyz and source per wheel,
+// then the cell reference of the deepest arena contact.
 // kWsBest: cell reference of the deepest arena contact (-1: none); kWsMan:
 // that contact as a manifold point (car-local point xyz, world point xyz,
 // world normal xyz, signed distance)
 enum : int { kWsDist = 0, kWsNx = 4, kWsNy = 8, kWsNz = 12, kWsSrc = 16, kWsBest = 20, kWsMan = 21, kWsPlanes = 31 };
+
+// The workspace is tiled like the persistent state (64 cars per tile, the
+// planes of a tile adjacent) and accessed with buffer loads and stores.
+DI __amdgpu_buffer_rsrc_t wsRsrc(const uint32_t* ws, int n)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(ws), 0, (int)(4u * kWsPlanes * tiledItems(n)),
+                                             0x00020000);
+}
+DI uint32_t wsGet(const uint32_t* ws, int n, int plane, int car)
+{
+    return __builtin_amdgcn_raw_buffer_load_b32(wsRsrc(ws, n), Dev::itemOff(car, kWsPlanes), plane * 256, 0);
+}
+DI void wsPut(uint32_t* ws, int n, int plane, int car, uint32_t v)
+{
+    __builtin_amdgcn_raw_buffer_store_b32(v, wsRsrc(ws, n), Dev::itemOff(car, kWsPlanes), plane * 256, 0);
+}
 
 // Simulations [begin, end) of one launch: the tick runs as independent
 // partitions on separate streams so the tail of one partition's kernel
@@ -106,19 +122,19 @@ DI void contactGroup(const Dev& d, uint32_t* __restrict__ ws, int screen, int ca
     if (!ok) return;
     Wheels w;
     const int best = contactFinish(d, L, lane, car, car / d.nCars, cen, rot, w);
-    const size_t n = d.nTotal;
+    const int n = d.nTotal;
 #pragma unroll
     for (int k = 0; k < kWheels; k++) {
-        ws[(kWsDist + k) * n + car] = __float_as_uint(w.dist[k]);
-        ws[(kWsNx + k) * n + car] = __float_as_uint(w.normal[k].x);
-        ws[(kWsNy + k) * n + car] = __float_as_uint(w.normal[k].y);
-        ws[(kWsNz + k) * n + car] = __float_as_uint(w.normal[k].z);
-        ws[(kWsSrc + k) * n + car] = (uint32_t)w.src[k];
+        wsPut(ws, n, kWsDist + k, car, __float_as_uint(w.dist[k]));
+        wsPut(ws, n, kWsNx + k, car, __float_as_uint(w.normal[k].x));
+        wsPut(ws, n, kWsNy + k, car, __float_as_uint(w.normal[k].y));
+        wsPut(ws, n, kWsNz + k, car, __float_as_uint(w.normal[k].z));
+        wsPut(ws, n, kWsSrc + k, car, (uint32_t)w.src[k]);
     }
-    ws[kWsBest * n + car] = (uint32_t)best;
+    wsPut(ws, n, kWsBest, car, (uint32_t)best);
     if (best >= 0) {
 #pragma unroll
-        for (int i = 0; i < 10; i++) ws[(kWsMan + i) * n + car] = __float_as_uint(L.bestPt[i][lane]);
+        for (int i = 0; i < 10; i++) wsPut(ws, n, kWsMan + i, car, __float_as_uint(L.bestPt[i][lane]));
     }
 }
 
@@ -134,21 +150,21 @@ __global__ __launch_bounds__(kContactBlock) void contactKernel(Dev d, uint32_t* 
 DI void carArenaCar(const Dev& d, const uint32_t* __restrict__ ws, int kind, const void* __restrict__ actions,
                     int tick, int car)
 {
-    const size_t n = d.nTotal;
+    const int n = d.nTotal;
     Wheels w;
 #pragma unroll
     for (int k = 0; k < kWheels; k++) {
-        w.dist[k] = __uint_as_float(ws[(kWsDist + k) * n + car]);
-        w.normal[k] = V3{ __uint_as_float(ws[(kWsNx + k) * n + car]), __uint_as_float(ws[(kWsNy + k) * n + car]),
-                          __uint_as_float(ws[(kWsNz + k) * n + car]) };
-        w.src[k] = (int)ws[(kWsSrc + k) * n + car];
+        w.dist[k] = __uint_as_float(wsGet(ws, n, kWsDist + k, car));
+        w.normal[k] = V3{ __uint_as_float(wsGet(ws, n, kWsNx + k, car)), __uint_as_float(wsGet(ws, n, kWsNy + k, car)),
+                          __uint_as_float(wsGet(ws, n, kWsNz + k, car)) };
+        w.src[k] = (int)wsGet(ws, n, kWsSrc + k, car);
     }
-    const int best = (int)ws[kWsBest * n + car];
+    const int best = (int)wsGet(ws, n, kWsBest, car);
     ManPt bestPt{};
     if (best >= 0) {
         float v[10];
 #pragma unroll
-        for (int i = 0; i < 10; i++) v[i] = __uint_as_float(ws[(kWsMan + i) * n + car]);
+        for (int i = 0; i < 10; i++) v[i] = __uint_as_float(wsGet(ws, n, kWsMan + i, car));
         bestPt = ManPt{ V3{ v[0], v[1], v[2] }, V3{ v[3], v[4], v[5] }, V3{ v[6], v[7], v[8] }, v[9] };
     }
     const Controls ctl = decodeControls(kind, actions, car);
@@ -1078,8 +1094,8 @@ int carl_env_create(int nSim, int nBlue, int nOrange, int seed, int frameskip, i
     }
     const size_t nT = (size_t)e->nTotal, nS = (size_t)nSim;
     int rc = CARL_OK;
-    rc = rc ? rc : devAlloc(&e->car, (size_t)CARL_CAR_FIELDS * nT);
-    rc = rc ? rc : devAlloc(&e->sim, (size_t)CARL_SIM_FIELDS * nS);
+    rc = rc ? rc : devAlloc(&e->car, (size_t)CARL_CAR_FIELDS * tiledItems(e->nTotal));
+    rc = rc ? rc : devAlloc(&e->sim, (size_t)CARL_SIM_FIELDS * tiledItems(nSim));
     rc = rc ? rc : devAlloc(&e->rec, host.records.size() / 4);
     rc = rc ? rc : devAlloc(&e->cellStart, host.cellStart.size());
     rc = rc ? rc : devAlloc(&e->angles, host.angles.size() / 3);
@@ -1103,7 +1119,7 @@ int carl_env_create(int nSim, int nBlue, int nOrange, int seed, int frameskip, i
     rc = rc ? rc : devAlloc(&e->tticks, nS);
     rc = rc ? rc : devAlloc(&e->actions, nT * 7);
     rc = rc ? rc : devAlloc(&e->cactions, nT * 7);
-    rc = rc ? rc : devAlloc(&e->ws, nT * kWsPlanes);
+    rc = rc ? rc : devAlloc(&e->ws, (size_t)kWsPlanes * tiledItems(e->nTotal));
     if (rc) return bail(rc);
 
     std::vector<float4> ang(host.angles.size() / 3);
@@ -1399,8 +1415,16 @@ int carl_env_export_state(carl_env* e, uint32_t* car, uint32_t* sim, int* tick)
 {
     CARL_TRY(checkEnv(e));
     HIP_TRY(hipStreamSynchronize(e->stream));
-    if (car) HIP_TRY(hipMemcpy(car, e->car, sizeof(uint32_t) * CARL_CAR_FIELDS * (size_t)e->nTotal, hipMemcpyDeviceToHost));
-    if (sim) HIP_TRY(hipMemcpy(sim, e->sim, sizeof(uint32_t) * CARL_SIM_FIELDS * (size_t)e->nSim, hipMemcpyDeviceToHost));
+    // device tiles of 64 items -> planes (field f, item i at f * n + i)
+    auto untile = [](const uint32_t* dev, uint32_t* out, int fields, int n) -> int {
+        std::vector<uint32_t> tiles((size_t)fields * tiledItems(n));
+        HIP_TRY(hipMemcpy(tiles.data(), dev, tiles.size() * sizeof(uint32_t), hipMemcpyDeviceToHost));
+        for (int f = 0; f < fields; f++)
+            for (int i = 0; i < n; i++) out[(size_t)f * n + i] = tiles[tiledWord(f, i, fields)];
+        return CARL_OK;
+    };
+    if (car) CARL_TRY(untile(e->car, car, CARL_CAR_FIELDS, e->nTotal));
+    if (sim) CARL_TRY(untile(e->sim, sim, CARL_SIM_FIELDS, e->nSim));
     if (tick) *tick = e->tickCount;
     return CARL_OK;
 }
@@ -1410,8 +1434,16 @@ int carl_env_import_state(carl_env* e, const uint32_t* car, const uint32_t* sim,
     CARL_TRY(checkEnv(e));
     if (!car || !sim) return fail(CARL_ERR_VALUE, "null state buffer");
     HIP_TRY(hipStreamSynchronize(e->stream));
-    HIP_TRY(hipMemcpy(e->car, car, sizeof(uint32_t) * CARL_CAR_FIELDS * (size_t)e->nTotal, hipMemcpyHostToDevice));
-    HIP_TRY(hipMemcpy(e->sim, sim, sizeof(uint32_t) * CARL_SIM_FIELDS * (size_t)e->nSim, hipMemcpyHostToDevice));
+    // planes -> device tiles of 64 items (the padding items stay zero)
+    auto tile = [](const uint32_t* in, uint32_t* dev, int fields, int n) -> int {
+        std::vector<uint32_t> tiles((size_t)fields * tiledItems(n), 0u);
+        for (int f = 0; f < fields; f++)
+            for (int i = 0; i < n; i++) tiles[tiledWord(f, i, fields)] = in[(size_t)f * n + i];
+        HIP_TRY(hipMemcpy(dev, tiles.data(), tiles.size() * sizeof(uint32_t), hipMemcpyHostToDevice));
+        return CARL_OK;
+    };
+    CARL_TRY(tile(car, e->car, CARL_CAR_FIELDS, e->nTotal));
+    CARL_TRY(tile(sim, e->sim, CARL_SIM_FIELDS, e->nSim));
     e->tickCount = tick;
     return CARL_OK;
 }

@@ -1,10 +1,15 @@
 // state.h - device views of the environment state and the arena.
 //
-// Persistent state lives in two structure-of-arrays blocks of 32-bit words:
-// car plane f, car c at car[f * nTotal + c]; sim plane f, sim s at
-// sim[f * nSim + s] (field numbering of include/carl_amd.h).  A wavefront of
-// 64 consecutive cars therefore reads every field as one contiguous 256-byte
-// segment.  Cars of one simulation are adjacent (c = s * nCars + local).
+// Persistent state lives in two blocks of 32-bit words, cars and simulations
+// (field numbering of include/carl_amd.h), each in tiles of 64 items: field f
+// of item i is word ((i / 64) * fields + f) * 64 + i % 64.  A wavefront of 64
+// consecutive cars therefore reads every field as one contiguous 256-byte
+// segment, and the accessors below address a field with a buffer load whose
+// per-item part is one 32-bit offset shared by every field of the item and
+// whose field part is a constant (immediate offset plus a constant scalar
+// offset): no 64-bit address and no per-field base pointer is formed.  Cars
+// of one simulation are adjacent (c = s * nCars + local).  Export and import
+// convert to and from the plane layout of the C-ABI.
 //
 // The arena is stored per grid cell: the triangles registered in a cell are a
 // contiguous run of 64-byte records (four float4, one per half cache line
@@ -80,26 +85,46 @@ HDI void cellOf(V3 p, int& cx, int& cy, int& cz)
 }
 HDI int flatCell(int cx, int cy, int cz) { return cx + cy * kGridX + cz * kGridX * kGridY; }
 
+// Items rounded up to whole tiles of 64, and the word of (field, item).
+HDI unsigned tiledItems(int n) { return ((unsigned)n + 63u) & ~63u; }
+HDI size_t tiledWord(int f, int i, int fields) { return ((size_t)(i >> 6) * fields + f) * 64 + (i & 63); }
+
 struct Dev {
     uint32_t* car;
     uint32_t* sim;
     int nSim, nBlue, nCars, nTotal, seed;
     ArenaView arena;
 
-    DI float cf(int f, int i) const { return __uint_as_float(car[(size_t)f * nTotal + i]); }
-    DI int ci(int f, int i) const { return (int)car[(size_t)f * nTotal + i]; }
+    // Raw buffer resources over the two blocks (dword 3: the gfx9 raw-buffer
+    // format); accesses past the end read 0 and store nothing.
+    DI __amdgpu_buffer_rsrc_t carRsrc() const
+    {
+        return __builtin_amdgcn_make_buffer_rsrc(car, 0, (int)(4u * CARL_CAR_FIELDS * tiledItems(nTotal)), 0x00020000);
+    }
+    DI __amdgpu_buffer_rsrc_t simRsrc() const
+    {
+        return __builtin_amdgcn_make_buffer_rsrc(sim, 0, (int)(4u * CARL_SIM_FIELDS * tiledItems(nSim)), 0x00020000);
+    }
+    static DI int itemOff(int i, int fields) { return ((i >> 6) * fields * 64 + (i & 63)) * 4; }
+    DI uint32_t cw(int f, int i) const { return __builtin_amdgcn_raw_buffer_load_b32(carRsrc(), itemOff(i, CARL_CAR_FIELDS), f * 256, 0); }
+    DI uint32_t sw(int f, int s) const { return __builtin_amdgcn_raw_buffer_load_b32(simRsrc(), itemOff(s, CARL_SIM_FIELDS), f * 256, 0); }
+    DI void cput(int f, int i, uint32_t v) const { __builtin_amdgcn_raw_buffer_store_b32(v, carRsrc(), itemOff(i, CARL_CAR_FIELDS), f * 256, 0); }
+    DI void sput(int f, int s, uint32_t v) const { __builtin_amdgcn_raw_buffer_store_b32(v, simRsrc(), itemOff(s, CARL_SIM_FIELDS), f * 256, 0); }
+
+    DI float cf(int f, int i) const { return __uint_as_float(cw(f, i)); }
+    DI int ci(int f, int i) const { return (int)cw(f, i); }
     DI V3 cv(int f, int i) const { return V3{ cf(f, i), cf(f + 1, i), cf(f + 2, i) }; }
     DI Q4 cq(int f, int i) const { return Q4{ cf(f, i), cf(f + 1, i), cf(f + 2, i), cf(f + 3, i) }; }
-    DI void setf(int f, int i, float v) const { car[(size_t)f * nTotal + i] = __float_as_uint(v); }
-    DI void seti(int f, int i, int v) const { car[(size_t)f * nTotal + i] = (uint32_t)v; }
+    DI void setf(int f, int i, float v) const { cput(f, i, __float_as_uint(v)); }
+    DI void seti(int f, int i, int v) const { cput(f, i, (uint32_t)v); }
     DI void setv(int f, int i, V3 v) const { setf(f, i, v.x); setf(f + 1, i, v.y); setf(f + 2, i, v.z); }
     DI void setq(int f, int i, Q4 q) const { setf(f, i, q.x); setf(f + 1, i, q.y); setf(f + 2, i, q.z); setf(f + 3, i, q.w); }
 
-    DI float sf(int f, int s) const { return __uint_as_float(sim[(size_t)f * nSim + s]); }
-    DI int si(int f, int s) const { return (int)sim[(size_t)f * nSim + s]; }
+    DI float sf(int f, int s) const { return __uint_as_float(sw(f, s)); }
+    DI int si(int f, int s) const { return (int)sw(f, s); }
     DI V3 sv(int f, int s) const { return V3{ sf(f, s), sf(f + 1, s), sf(f + 2, s) }; }
-    DI void ssetf(int f, int s, float v) const { sim[(size_t)f * nSim + s] = __float_as_uint(v); }
-    DI void sseti(int f, int s, int v) const { sim[(size_t)f * nSim + s] = (uint32_t)v; }
+    DI void ssetf(int f, int s, float v) const { sput(f, s, __float_as_uint(v)); }
+    DI void sseti(int f, int s, int v) const { sput(f, s, (uint32_t)v); }
     DI void ssetv(int f, int s, V3 v) const { ssetf(f, s, v.x); ssetf(f + 1, s, v.y); ssetf(f + 2, s, v.z); }
 };
 
