@@ -1,15 +1,21 @@
-"""Named tensor views over CARL's packed observation and state layouts.
+"""Named views over the packed observation and state rows, and the records
+the vector environment passes to reward functions and reset providers.
 
-API-compatible with the reference views (python/carl/gymnasium/state.py:10-530):
-the same classes and properties, each a slice that shares storage with the
-packed tensor.  Offsets come from the module constants, which restate the
-layout contract of include/Cuda/DLPack.h:60-107.
+Interface (class names, attribute names, the slices they return, the
+reset-state contract): python/carl/gymnasium/state.py:10-530.  Column
+positions come from the native module's constants, which restate the layout
+of include/Cuda/DLPack.h:60-107.
+
+Every named view is a descriptor generated from one of three field tables
+(car, ball, observation row), so each layout is written down once and every
+view is a slice that shares storage with the packed tensor.
 """
 from __future__ import annotations
 
+import functools
 from collections.abc import Mapping
 from dataclasses import dataclass, field
-from typing import Any
+from typing import Any, NamedTuple
 
 import torch as th
 
@@ -17,14 +23,60 @@ import carl_amd as carl
 from carl_amd import BOOST_PAD_POSITIONS, REGULATION_TICKS
 
 
-@dataclass(frozen=True)
-class RewardResult:
-    reward: th.Tensor
-    info: Mapping[str, list[Any]] = field(default_factory=dict)
+class _Cols:
+    """Descriptor: columns [start, stop) of the last axis, or column `start`
+    alone when stop is None (as bool when `flag`).  `via` names an attribute
+    of the owner whose value is sliced instead of the owner itself."""
+
+    def __init__(self, start: int, stop: int | None = None, *, flag: bool = False, via: str | None = None,
+                 doc: str = ""):
+        self.start, self.stop, self.flag, self.via = start, stop, flag, via
+        self.__doc__ = doc
+
+    def __get__(self, obj, owner=None):
+        if obj is None:
+            return self
+        base = getattr(obj, self.via) if self.via else obj
+        cols = base[..., self.start] if self.stop is None else base[..., self.start:self.stop]
+        return cols.bool() if self.flag else cols
 
 
-class _CARLTensor(th.Tensor):
-    """Tensor subclass whose torch operations return plain tensors."""
+class _Field(NamedTuple):
+    name: str
+    start: int
+    stop: int | None
+    flag: bool
+    doc: str
+
+
+# columns of one car (observation car block; the canonical state's car rows
+# carry the same columns plus the ball-touch flag)
+_PHYSICS_FIELDS = (
+    _Field("position", carl.OBS_POS, carl.OBS_VEL, False, "position (uu)"),
+    _Field("velocity", carl.OBS_VEL, carl.OBS_ANG, False, "linear velocity (uu/s)"),
+    _Field("angular_velocity", carl.OBS_ANG, carl.OBS_FORWARD, False, "angular velocity (rad/s)"),
+)
+_CAR_FIELDS = _PHYSICS_FIELDS + (
+    _Field("forward", carl.OBS_FORWARD, carl.OBS_UP, False, "unit forward axis"),
+    _Field("up", carl.OBS_UP, carl.OBS_BOOST, False, "unit up axis"),
+    _Field("boost", carl.OBS_BOOST, None, False, "boost amount [0, 100]"),
+    _Field("on_ground", carl.OBS_ON_GROUND, None, True, "three or more wheels touching"),
+    _Field("demoed", carl.OBS_DEMOED, None, True, "demolished, waiting to respawn"),
+    _Field("has_flipped", carl.OBS_HAS_FLIPPED, None, True, "the flip of this jump is used"),
+    _Field("has_double_jumped", carl.OBS_HAS_DOUBLE_JUMPED, None, True, "the double jump is used"),
+    _Field("is_boosting", carl.OBS_IS_BOOSTING, None, True, "boosting this tick"),
+)
+
+
+def _install(cls, fields, *, prefix: str = "", via: str | None = None):
+    for f in fields:
+        setattr(cls, prefix + f.name, _Cols(f.start, f.stop, flag=f.flag, via=via, doc=f.doc))
+    return cls
+
+
+class _Packed(th.Tensor):
+    """Tensor subclass whose torch operations return plain tensors; only the
+    named views keep the subclass."""
 
     @classmethod
     def from_tensor(cls, tensor: th.Tensor):
@@ -36,39 +88,21 @@ class _CARLTensor(th.Tensor):
             return func(*args, **(kwargs or {}))
 
 
-def _span(start: int, stop: int, doc: str):
-    return property(lambda self: self[..., start:stop], doc=doc)
+@functools.partial(_install, fields=_PHYSICS_FIELDS)
+class CARLBall(_Packed):
+    """[..., OBS_BALL] ball columns: position, velocity, angular velocity."""
 
 
-def _scalar(index: int, doc: str, as_bool: bool = False):
-    if as_bool:
-        return property(lambda self: self[..., index].bool(), doc=doc)
-    return property(lambda self: self[..., index], doc=doc)
-
-
-class _CARLPhysics(_CARLTensor):
-    position = _span(carl.OBS_POS, carl.OBS_VEL, "position (uu)")
-    velocity = _span(carl.OBS_VEL, carl.OBS_ANG, "linear velocity (uu/s)")
-    angular_velocity = _span(carl.OBS_ANG, carl.OBS_FORWARD, "angular velocity (rad/s)")
-
-
-class CARLBall(_CARLPhysics):
-    pass
-
-
-class CARLCar(_CARLPhysics):
-    forward = _span(carl.OBS_FORWARD, carl.OBS_UP, "forward axis")
-    up = _span(carl.OBS_UP, carl.OBS_BOOST, "up axis")
-    boost = _scalar(carl.OBS_BOOST, "boost amount")
-    on_ground = _scalar(carl.OBS_ON_GROUND, "three or more wheels in contact", True)
-    demoed = _scalar(carl.OBS_DEMOED, "demolished", True)
-    has_flipped = _scalar(carl.OBS_HAS_FLIPPED, "flip used", True)
-    has_double_jumped = _scalar(carl.OBS_HAS_DOUBLE_JUMPED, "double jump used", True)
-    is_boosting = _scalar(carl.OBS_IS_BOOSTING, "boosting", True)
+@functools.partial(_install, fields=_CAR_FIELDS)
+class CARLCar(_Packed):
+    """[..., OBS_PER_CAR] columns of one car."""
 
 
 class CARLCars(CARLCar):
-    """[..., n_cars, OBS_PER_CAR] view; car 0 is the observer."""
+    """[..., n_cars, OBS_PER_CAR]: every car of an observation, the observer
+    first, then its teammates, then the opponents."""
+
+    _n_cars: int
 
     @staticmethod
     def from_tensor(tensor: th.Tensor, n_cars: int) -> "CARLCars":
@@ -84,16 +118,43 @@ class CARLCars(CARLCar):
     def ego(self) -> CARLCar:
         return CARLCar.from_tensor(self[..., 0, :])
 
-    ego_position = property(lambda self: self.ego.position)
-    ego_velocity = property(lambda self: self.ego.velocity)
-    ego_angular_velocity = property(lambda self: self.ego.angular_velocity)
-    ego_forward = property(lambda self: self.ego.forward)
-    ego_up = property(lambda self: self.ego.up)
-    ego_boost = property(lambda self: self.ego.boost)
+
+_install(CARLCars, [f for f in _CAR_FIELDS if f.name in ("position", "velocity", "angular_velocity", "forward",
+                                                          "up", "boost")], prefix="ego_", via="ego")
 
 
-class CARLObservation(_CARLTensor):
-    """One agent's packed observation with named views."""
+class _ObsColumns(NamedTuple):
+    """Start columns of the blocks of an observation row with n cars."""
+    car_end: int
+    pads_active: int
+    pads_distance: int
+    ego_ball: int
+    others: int
+    own_goal: int
+    opponent_goal: int
+    dodge: int
+    controller: int
+    previous: int
+
+
+@functools.lru_cache(maxsize=None)
+def _obs_columns(n_cars: int) -> _ObsColumns:
+    car_end = carl.OBS_BALL + carl.OBS_PER_CAR * n_cars
+    ego_ball = car_end + carl.OBS_BOOST_PADS
+    others = ego_ball + carl.OBS_RELATIVE_EGO_BALL
+    own_goal = others + carl.OBS_RELATIVE_PER_OTHER_CAR * (n_cars - 1)
+    dodge = own_goal + carl.OBS_RELATIVE_GOALS
+    controller = dodge + carl.OBS_EGO_DODGE
+    return _ObsColumns(car_end=car_end, pads_active=car_end, pads_distance=car_end + carl.NUM_BOOST_PADS,
+                       ego_ball=ego_ball, others=others, own_goal=own_goal,
+                       opponent_goal=own_goal + carl.OBS_VECTOR_SIZE, dodge=dodge, controller=controller,
+                       previous=controller + carl.OBS_EGO_CONTROLLER)
+
+
+class CARLObservation(_Packed):
+    """Observation rows [..., obs_dim] with named views of the packed layout:
+    ball, cars, boost pads, relative vectors, goals, dodge window,
+    controller state and the optional previous controls."""
 
     _n_cars: int
 
@@ -108,124 +169,145 @@ class CARLObservation(_CARLTensor):
         return self._n_cars
 
     @property
-    def car_end(self) -> int:
-        return carl.OBS_BALL + carl.OBS_PER_CAR * self._n_cars
+    def _cols(self) -> _ObsColumns:
+        return _obs_columns(self._n_cars)
 
-    # ball
+    def _block(self, start: int, width: int) -> th.Tensor:
+        return self[..., start:start + width]
+
+    @property
+    def car_end(self) -> int:
+        return self._cols.car_end
+
     @property
     def ball(self) -> CARLBall:
         return CARLBall.from_tensor(self[..., :carl.OBS_BALL])
 
-    ball_values = property(lambda self: self.ball)
-    ball_position = property(lambda self: self.ball.position)
-    ball_velocity = property(lambda self: self.ball.velocity)
-    ball_angular_velocity = property(lambda self: self.ball.angular_velocity)
-
-    # cars: observer, teammates, opponents
     @property
     def cars(self) -> CARLCars:
-        flat = self[..., carl.OBS_BALL:self.car_end]
-        return CARLCars.from_tensor(flat.view(*self.shape[:-1], self._n_cars, carl.OBS_PER_CAR), self._n_cars)
+        block = self[..., carl.OBS_BALL:self._cols.car_end]
+        return CARLCars.from_tensor(block.view(*self.shape[:-1], self._n_cars, carl.OBS_PER_CAR), self._n_cars)
 
+    ball_values = property(lambda self: self.ball)
     car_values = property(lambda self: self.cars)
     ego_values = property(lambda self: self.cars.ego)
-    car_position = property(lambda self: self.cars.position)
-    car_velocity = property(lambda self: self.cars.velocity)
-    car_angular_velocity = property(lambda self: self.cars.angular_velocity)
-    car_forward = property(lambda self: self.cars.forward)
-    car_up = property(lambda self: self.cars.up)
-    car_boost = property(lambda self: self.cars.boost)
-    car_on_ground = property(lambda self: self.cars.on_ground)
-    car_demoed = property(lambda self: self.cars.demoed)
-    car_has_flipped = property(lambda self: self.cars.has_flipped)
-    car_has_double_jumped = property(lambda self: self.cars.has_double_jumped)
-    car_is_boosting = property(lambda self: self.cars.is_boosting)
 
-    # boost pads
     @property
     def boost_pad_active(self) -> th.Tensor:
-        return self[..., self.car_end:self.car_end + carl.NUM_BOOST_PADS].bool()
+        return self._block(self._cols.pads_active, carl.NUM_BOOST_PADS).bool()
 
     @property
     def boost_pad_distance(self) -> th.Tensor:
-        start = self.car_end + carl.NUM_BOOST_PADS
-        return self[..., start:start + carl.NUM_BOOST_PADS]
+        return self._block(self._cols.pads_distance, carl.NUM_BOOST_PADS)
 
-    # relative vectors
     @property
     def ego_ball_relative(self) -> th.Tensor:
-        start = self.car_end + carl.OBS_BOOST_PADS
-        return self[..., start:start + carl.OBS_RELATIVE_EGO_BALL]
+        return self._block(self._cols.ego_ball, carl.OBS_RELATIVE_EGO_BALL)
 
     @property
     def ego_other_relative(self) -> th.Tensor:
-        start = self.car_end + carl.OBS_BOOST_PADS + carl.OBS_RELATIVE_EGO_BALL
-        stop = start + carl.OBS_RELATIVE_PER_OTHER_CAR * (self._n_cars - 1)
-        return self[..., start:stop].view(*self.shape[:-1], self._n_cars - 1, carl.OBS_RELATIVE_PER_OTHER_CAR)
-
-    @property
-    def _goal_start(self) -> int:
-        return (self.car_end + carl.OBS_BOOST_PADS + carl.OBS_RELATIVE_EGO_BALL
-                + carl.OBS_RELATIVE_PER_OTHER_CAR * (self._n_cars - 1))
+        others = self._n_cars - 1
+        block = self._block(self._cols.others, carl.OBS_RELATIVE_PER_OTHER_CAR * others)
+        return block.view(*self.shape[:-1], others, carl.OBS_RELATIVE_PER_OTHER_CAR)
 
     @property
     def own_goal_relative(self) -> th.Tensor:
-        return self[..., self._goal_start:self._goal_start + carl.OBS_VECTOR_SIZE]
+        return self._block(self._cols.own_goal, carl.OBS_VECTOR_SIZE)
 
     @property
     def opponent_goal_relative(self) -> th.Tensor:
-        start = self._goal_start + carl.OBS_VECTOR_SIZE
-        return self[..., start:start + carl.OBS_VECTOR_SIZE]
+        return self._block(self._cols.opponent_goal, carl.OBS_VECTOR_SIZE)
 
-    # dodge window and controller state
     @property
     def ego_has_flip_or_jump(self) -> th.Tensor:
-        return self[..., self._goal_start + carl.OBS_RELATIVE_GOALS].bool()
+        return self[..., self._cols.dodge].bool()
 
     @property
     def ego_flip_window_remaining(self) -> th.Tensor:
-        return self[..., self._goal_start + carl.OBS_RELATIVE_GOALS + 1]
+        return self[..., self._cols.dodge + 1]
 
     @property
     def ego_controller(self) -> th.Tensor:
-        start = self._goal_start + carl.OBS_RELATIVE_GOALS + carl.OBS_EGO_DODGE
-        stop = start + carl.OBS_EGO_CONTROLLER
-        if self.shape[-1] not in (stop, stop + carl.OBS_PREVIOUS_CONTROLS):
+        cols = self._cols
+        if self.shape[-1] not in (cols.previous, cols.previous + carl.OBS_PREVIOUS_CONTROLS):
             raise ValueError("observation does not match ego controller v3")
-        return self[..., start:stop]
+        return self[..., cols.controller:cols.previous]
 
     @property
     def ego_previous_controls(self) -> th.Tensor:
-        self.ego_controller  # validates the layout
-        start = self._goal_start + carl.OBS_RELATIVE_GOALS + carl.OBS_EGO_DODGE + carl.OBS_EGO_CONTROLLER
-        if self.shape[-1] != start + carl.OBS_PREVIOUS_CONTROLS:
+        cols = self._cols
+        if self.shape[-1] != cols.previous + carl.OBS_PREVIOUS_CONTROLS:
+            if self.shape[-1] != cols.previous:
+                raise ValueError("observation does not match ego controller v3")
             raise ValueError("observation does not include previous controls")
-        return self[..., start:]
+        return self[..., cols.previous:]
 
-    ego_has_jumped = property(lambda self: self.ego_controller[..., 0].bool())
-    ego_is_jumping = property(lambda self: self.ego_controller[..., 1].bool())
-    ego_is_flipping = property(lambda self: self.ego_controller[..., 2].bool())
-    ego_flip_time = property(lambda self: self.ego_controller[..., 3])
-    ego_demo_respawn_time = property(lambda self: self.ego_controller[..., 4])
+
+_install(CARLObservation, _PHYSICS_FIELDS, prefix="ball_", via="ball")
+_install(CARLObservation, _CAR_FIELDS, prefix="car_", via="cars")
+_install(CARLObservation, (
+    _Field("has_jumped", 0, None, True, "jumped since the last landing"),
+    _Field("is_jumping", 1, None, True, "jump impulse still applied"),
+    _Field("is_flipping", 2, None, True, "a flip is in progress"),
+    _Field("flip_time", 3, None, False, "seconds since the flip started"),
+    _Field("demo_respawn_time", 4, None, False, "seconds until the respawn"),
+), prefix="ego_", via="ego_controller")
 
 
 @dataclass(frozen=True)
 class CARLMatchReset:
-    """Match state of the simulations a reset provider restores."""
+    """Scores and episode clock for the simulations a reset restores."""
 
     blue_score: th.Tensor
     orange_score: th.Tensor
     episode_ticks: th.Tensor
 
 
+def _column_scale(pairs) -> tuple[float, ...]:
+    """Per-column factors from (width, factor or factors) runs."""
+    out: list[float] = []
+    for width, factor in pairs:
+        out.extend(factor if isinstance(factor, tuple) else (factor,) * width)
+    return tuple(out)
+
+
+# normalised -> physics units, column by column (1 where no normalisation applies)
+_BALL_SCALE = _column_scale(((3, tuple(carl.OBS_POSITION_SCALE)), (3, carl.BALL_MAX_SPEED),
+                             (3, carl.BALL_MAX_ANG_SPEED)))
+_CAR_SCALE = _column_scale(((3, tuple(carl.OBS_POSITION_SCALE)), (3, carl.CAR_MAX_SPEED),
+                            (3, carl.CAR_MAX_ANG_SPEED), (carl.OBS_BOOST - carl.OBS_FORWARD, 1.0),
+                            (1, carl.BOOST_MAX), (carl.OBS_PER_CAR - carl.OBS_BOOST - 1, 1.0)))
+assert len(_BALL_SCALE) == carl.OBS_BALL and len(_CAR_SCALE) == carl.OBS_PER_CAR
+
+
+def _is_arena_mask(mask: th.Tensor, eligible: th.Tensor) -> bool:
+    return mask.shape == eligible.shape and mask.dtype == th.bool and mask.device == eligible.device
+
+
+def _check_indices(indices: th.Tensor | None, eligible: th.Tensor) -> None:
+    """Indexed selection: int64 vector on the environment's device, in range,
+    without repeats, naming only arenas that are eligible for a reset."""
+    if indices is None or indices.ndim != 1 or indices.dtype != th.int64 or indices.device != eligible.device:
+        raise ValueError("simulation_indices must be int64 on the environment device")
+    n = len(eligible)
+    if indices.numel() == 0:
+        return
+    if int(indices.min()) < 0 or int(indices.max()) >= n:
+        raise ValueError("simulation_indices are out of range")
+    hits = th.bincount(indices, minlength=n)
+    if bool((hits > 1).any()) or bool((hits.bool() & ~eligible).any()):
+        raise ValueError("simulation_indices must be unique and selected for reset")
+
+
 @dataclass(frozen=True)
 class CARLResetState:
-    """Reset state in physics units (or normalised units when ``normalized``).
+    """State a reset provider returns, in physics units, or in the
+    observation's normalised units when `normalized`.
 
-    Indexed form: ``simulation_indices`` (int64) names the rows.  Fixed-shape
-    form: ``simulation_indices=None`` and a bool ``reset_mask`` [n_sim]; every
-    tensor then has one row per arena and only metadata is validated on the
-    host.
+    Either `simulation_indices` (int64) names one row per restored arena, or
+    `simulation_indices` is None and the bool `reset_mask` [n_sim] selects
+    arenas from full-size rows; that fixed-shape form is validated from its
+    metadata only (no host readback), so its rotations must be valid.
     """
 
     simulation_indices: th.Tensor | None
@@ -236,58 +318,38 @@ class CARLResetState:
     normalized: bool = False
     reset_mask: th.Tensor | None = None
 
-    def validate(self, reset_mask: th.Tensor, n_cars: int) -> None:
-        rows = len(reset_mask)
-        if self.reset_mask is not None:
-            if self.simulation_indices is not None:
-                raise ValueError("specify reset_mask or simulation_indices, not both")
-            mask = self.reset_mask
-            if mask.shape != reset_mask.shape or mask.dtype != th.bool or mask.device != reset_mask.device:
-                raise ValueError("reset_mask must be bool [n_sim] on the environment device")
-        else:
-            self._validate_indices(reset_mask)
-            rows = len(self.simulation_indices)
-        if self.ball.shape != (rows, carl.OBS_BALL) or self.cars.shape != (rows, n_cars, carl.OBS_PER_CAR):
-            raise ValueError("ball or cars have the wrong shape")
+    def _rows(self, eligible: th.Tensor) -> int:
+        if self.reset_mask is None:
+            _check_indices(self.simulation_indices, eligible)
+            return len(self.simulation_indices)
+        if self.simulation_indices is not None:
+            raise ValueError("specify reset_mask or simulation_indices, not both")
+        if not _is_arena_mask(self.reset_mask, eligible):
+            raise ValueError("reset_mask must be bool [n_sim] on the environment device")
+        return len(eligible)
 
-    def _validate_indices(self, reset_mask: th.Tensor) -> None:
-        idx = self.simulation_indices
-        if idx is None or idx.ndim != 1 or idx.dtype != th.int64 or idx.device != reset_mask.device:
-            raise ValueError("simulation_indices must be int64 on the environment device")
-        if ((idx < 0) | (idx >= len(reset_mask))).any():
-            raise ValueError("simulation_indices are out of range")
-        if not reset_mask[idx].all() or th.unique(idx).numel() != len(idx):
-            raise ValueError("simulation_indices must be unique and selected for reset")
+    def validate(self, reset_mask: th.Tensor, n_cars: int) -> None:
+        rows = self._rows(reset_mask)
+        want = ((rows, carl.OBS_BALL), (rows, n_cars, carl.OBS_PER_CAR))
+        if (tuple(self.ball.shape), tuple(self.cars.shape)) != want:
+            raise ValueError("ball or cars have the wrong shape")
 
     def physical(self) -> tuple[CARLBall, CARLCars]:
         if not self.normalized:
             return self.ball, self.cars
-        ball = CARLBall.from_tensor(self.ball.clone())
-        cars = CARLCars.from_tensor(self.cars.clone(), self.cars.n_cars)
-        scale = ball.position.new_tensor(carl.OBS_POSITION_SCALE)
-        ball.position.mul_(scale)
-        ball.velocity.mul_(carl.BALL_MAX_SPEED)
-        ball.angular_velocity.mul_(carl.BALL_MAX_ANG_SPEED)
-        cars.position.mul_(scale)
-        cars.velocity.mul_(carl.CAR_MAX_SPEED)
-        cars.angular_velocity.mul_(carl.CAR_MAX_ANG_SPEED)
-        cars.boost.mul_(carl.BOOST_MAX)
+        ball = CARLBall.from_tensor(self.ball * self.ball.new_tensor(_BALL_SCALE))
+        cars = CARLCars.from_tensor(self.cars * self.cars.new_tensor(_CAR_SCALE), self.cars.n_cars)
         return ball, cars
 
 
-def _state_span(start: int, stop: int):
-    return property(lambda self: self.car_values[..., start:stop])
-
-
-def _state_flag(index: int, as_bool: bool = True):
-    if as_bool:
-        return property(lambda self: self.car_values[..., index].bool())
-    return property(lambda self: self.car_values[..., index])
+def _state_width(n_cars: int) -> int:
+    return carl.OBS_BALL + carl.STATE_PER_CAR * n_cars + carl.NUM_BOOST_PADS
 
 
 @dataclass(frozen=True)
 class CarlState:
-    """Canonical (un-mirrored) per-simulation state, [n_sim, state_dim]."""
+    """Canonical (never mirrored) state rows [n_sim, state_dim]: the ball,
+    every car in simulation order, then the boost pads."""
 
     raw: th.Tensor
     n_cars: int
@@ -297,36 +359,19 @@ class CarlState:
     @classmethod
     def from_raw(cls, raw: th.Tensor, n_cars: int, boost_pad_positions: th.Tensor,
                  team_sign: th.Tensor) -> "CarlState":
-        expected = carl.OBS_BALL + carl.STATE_PER_CAR * n_cars + carl.NUM_BOOST_PADS
-        if raw.ndim != 2 or raw.shape[1] != expected:
-            raise ValueError(f"Expected raw state shaped [n_sim, {expected}], got {tuple(raw.shape)}")
+        width = _state_width(n_cars)
+        if raw.ndim != 2 or raw.shape[1] != width:
+            raise ValueError(f"Expected raw state shaped [n_sim, {width}], got {tuple(raw.shape)}")
         return cls(raw, n_cars, boost_pad_positions, team_sign)
 
     @property
     def ball_values(self) -> th.Tensor:
         return self.raw[:, :carl.OBS_BALL]
 
-    ball_position = property(lambda self: self.ball_values[..., carl.OBS_POS:carl.OBS_VEL])
-    ball_velocity = property(lambda self: self.ball_values[..., carl.OBS_VEL:carl.OBS_ANG])
-    ball_angular_velocity = property(lambda self: self.ball_values[..., carl.OBS_ANG:carl.OBS_BALL])
-
     @property
     def car_values(self) -> th.Tensor:
-        stop = carl.OBS_BALL + carl.STATE_PER_CAR * self.n_cars
-        return self.raw[:, carl.OBS_BALL:stop].view(self.raw.shape[0], self.n_cars, carl.STATE_PER_CAR)
-
-    car_position = _state_span(carl.OBS_POS, carl.OBS_VEL)
-    car_velocity = _state_span(carl.OBS_VEL, carl.OBS_ANG)
-    car_angular_velocity = _state_span(carl.OBS_ANG, carl.OBS_FORWARD)
-    car_forward = _state_span(carl.OBS_FORWARD, carl.OBS_UP)
-    car_up = _state_span(carl.OBS_UP, carl.OBS_BOOST)
-    car_boost = _state_flag(carl.OBS_BOOST, as_bool=False)
-    car_on_ground = _state_flag(carl.OBS_ON_GROUND)
-    car_demoed = _state_flag(carl.OBS_DEMOED)
-    car_has_flipped = _state_flag(carl.OBS_HAS_FLIPPED)
-    car_has_double_jumped = _state_flag(carl.OBS_HAS_DOUBLE_JUMPED)
-    car_is_boosting = _state_flag(carl.OBS_IS_BOOSTING)
-    car_ball_touches = _state_flag(carl.STATE_BALL_TOUCH)
+        block = self.raw[:, carl.OBS_BALL:carl.OBS_BALL + carl.STATE_PER_CAR * self.n_cars]
+        return block.view(self.raw.shape[0], self.n_cars, carl.STATE_PER_CAR)
 
     @property
     def boost_pad_values(self) -> th.Tensor:
@@ -337,16 +382,29 @@ class CarlState:
         return self.boost_pad_values.bool()
 
 
-@dataclass(frozen=True)
+_install(CarlState, _PHYSICS_FIELDS, prefix="ball_", via="ball_values")
+_install(CarlState, _CAR_FIELDS + (
+    _Field("ball_touches", carl.STATE_BALL_TOUCH, None, True, "touched the ball within the step"),), prefix="car_",
+    via="car_values")
+
+
+@dataclass(frozen=True, slots=True)
 class CarlEvents:
+    """Per-arena outcome of the step: score change and how it ended."""
+
     score_delta: th.Tensor
     done: th.Tensor
     terminated: th.Tensor
     truncated: th.Tensor
 
 
-@dataclass(frozen=True)
+@dataclass(frozen=True, slots=True)
 class RewardContext:
+    """Everything a reward function sees for one step: the state before and
+    after it (`current` is the transition state, before any reset), the
+    observations around it, the step's events and actions, and the match
+    state at the end of the step."""
+
     current: CarlState
     previous: CarlState
     current_observation: CARLObservation
@@ -356,6 +414,14 @@ class RewardContext:
     score_difference: th.Tensor
     episode_ticks: th.Tensor
     overtime: th.Tensor
+
+
+@dataclass(frozen=True)
+class RewardResult:
+    """A reward function's [n_sim, n_cars] reward plus info entries."""
+
+    reward: th.Tensor
+    info: Mapping[str, list[Any]] = field(default_factory=dict)
 
 
 __all__ = [

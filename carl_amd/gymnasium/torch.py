@@ -1,26 +1,30 @@
 """Torch vector environment over the MI355X engine.
 
-API- and behaviour-compatible with CARLTorchVectorEnv
-(python/carl/gymnasium/torch.py:79-605):
-  * Gymnasium SAME_STEP autoreset: finished arenas are reset inside step();
-    terminated = done with a goal, truncated = done otherwise;
-  * default reward = per-step score delta * team sign, or the sum of
-    registered reward functions over a RewardContext;
-  * optional reset-state providers, indexed or fixed-shape (masked), applied
-    to finished arenas; masked providers never force a host synchronisation;
-  * episode return/length reporting, immediate or deferred.
-All engine work runs on the environment's private HIP stream; the torch
-current stream is joined to it around every native call.
+Interface and behaviour: python/carl/gymnasium/torch.py:79-605
+(CARLTorchVectorEnv): Gymnasium SAME_STEP autoreset (arenas that finish are
+reset inside step(); terminated = finished with a goal, truncated = finished
+otherwise), the default reward (score change x team sign) or the sum of
+registered reward functions over a RewardContext, optional reset-state
+providers (indexed, or fixed-shape with a mask and no host readback), and
+episode return/length reports, immediate or deferred to a rollout boundary.
+
+Structure: the environment composes three parts:
+  * `_StreamBridge` orders torch's current stream and the engine's private
+    stream around every native call;
+  * `_request_from_typed` / `_request_from_mapping` turn what a reset
+    provider returned (a CARLResetState or a mapping of tensors) into the
+    arguments of one `Env.apply_reset_state` call, or into none;
+  * `_EpisodeLedger` keeps the per-agent returns and lengths and produces the
+    episode reports.
 """
 from __future__ import annotations
 
 import math
 from collections.abc import Callable, Iterable, Mapping
-from typing import Any
+from typing import Any, NamedTuple
 
 import numpy as np
 import torch as th
-import torch.nn.functional as F
 
 import carl_amd as carl
 
@@ -42,53 +46,212 @@ ResetState = "CARLResetState | Mapping[str, th.Tensor]"
 ResetStateProvider = Callable[[th.Tensor], Any]
 
 
-def _forward_up_to_quat(forward: th.Tensor, up: th.Tensor, *, validate: bool = True) -> th.Tensor:
-    """Car axes -> unit quaternions in [x, y, z, w] order.
+# --------------------------------------------------------------- rotations
 
-    The basis is re-orthonormalised (right = up x forward, up = forward x
-    right) and converted with the sign-copy form of the matrix-to-quaternion
-    map: |q_i| from the diagonal, signs from the antisymmetric parts.
-    """
+def _forward_up_to_quat(forward: th.Tensor, up: th.Tensor, *, validate: bool = True) -> th.Tensor:
+    """Unit quaternions [x, y, z, w] (w >= 0) of the car frames whose local x
+    axis is `forward` and local z axis is `up` (re-orthonormalised: right =
+    up x forward, then up = forward x right).
+
+    Conversion by Shepperd's method (J. Guidance and Control 1(3), 1978): of
+    w, x, y, z the component with the largest magnitude is taken from the
+    square root of its diagonal combination and the other three from the
+    off-diagonal sums and differences divided by it, which keeps the division
+    well conditioned for every rotation."""
     right = th.linalg.cross(up, forward, dim=-1)
     if validate:
-        if not th.isfinite(forward).all() or not th.isfinite(up).all():
+        if not (th.isfinite(forward).all() and th.isfinite(up).all()):
             raise ValueError("car forward and up directions must be finite")
-        if (forward.square().sum(-1) < 1e-8).any() or (right.square().sum(-1) < 1e-8).any():
+        degenerate = (forward * forward).sum(-1).lt(1e-8) | (right * right).sum(-1).lt(1e-8)
+        if degenerate.any():
             raise ValueError("car forward and up directions must define a rotation")
-    f = F.normalize(forward, dim=-1)
-    r = F.normalize(right, dim=-1)
-    u = th.linalg.cross(f, r, dim=-1)
-    m = th.stack((f, r, u), dim=-1)  # columns: forward, right, up
-    m00, m11, m22 = m[..., 0, 0], m[..., 1, 1], m[..., 2, 2]
-    w = (1 + m00 + m11 + m22).clamp_min(0).sqrt()
-    x = th.copysign((1 + m00 - m11 - m22).clamp_min(0).sqrt(), m[..., 2, 1] - m[..., 1, 2])
-    y = th.copysign((1 - m00 + m11 - m22).clamp_min(0).sqrt(), m[..., 0, 2] - m[..., 2, 0])
-    z = th.copysign((1 - m00 - m11 + m22).clamp_min(0).sqrt(), m[..., 1, 0] - m[..., 0, 1])
-    return F.normalize(th.stack((x, y, z, w), dim=-1), dim=-1)
+    ex = forward / forward.norm(dim=-1, keepdim=True).clamp_min(1e-12)
+    ey = right / right.norm(dim=-1, keepdim=True).clamp_min(1e-12)
+    ez = th.linalg.cross(ex, ey, dim=-1)
+    # rotation matrix R = [ex ey ez] (columns); r[i][j] = R_ij
+    r = [[ex[..., i], ey[..., i], ez[..., i]] for i in range(3)]
+    trace = r[0][0] + r[1][1] + r[2][2]
+    # 4 q_k^2 for k = w, x, y, z
+    four_sq = th.stack((1 + trace, 1 + 2 * r[0][0] - trace, 1 + 2 * r[1][1] - trace, 1 + 2 * r[2][2] - trace), -1)
+    # pairwise products 4 q_a q_b
+    wx, wy, wz = r[2][1] - r[1][2], r[0][2] - r[2][0], r[1][0] - r[0][1]
+    xy, xz, yz = r[0][1] + r[1][0], r[0][2] + r[2][0], r[1][2] + r[2][1]
+    pick = four_sq.argmax(-1, keepdim=True)
+    big = four_sq.gather(-1, pick).clamp_min(0).sqrt()            # 2 |q_pick|
+    rows = th.stack((
+        th.stack((four_sq[..., 0], wx, wy, wz), -1),               # w largest: (4w^2, 4wx, 4wy, 4wz)
+        th.stack((wx, four_sq[..., 1], xy, xz), -1),               # x largest: (4xw, 4x^2, 4xy, 4xz)
+        th.stack((wy, xy, four_sq[..., 2], yz), -1),               # y largest
+        th.stack((wz, xz, yz, four_sq[..., 3]), -1),               # z largest
+    ), -2)
+    wxyz = rows.gather(-2, pick[..., None].expand(*pick.shape[:-1], 1, 4)).squeeze(-2) / (2 * big)
+    wxyz = wxyz / wxyz.norm(dim=-1, keepdim=True).clamp_min(1e-12)
+    wxyz = th.where(wxyz[..., :1] < 0, -wxyz, wxyz)
+    return wxyz[..., (1, 2, 3, 0)]
 
 
 def _ticks(ticks: int | None, seconds: float | None, default: int | None) -> int | None:
-    """Resolve a timeout given either in ticks or in seconds."""
+    """A timeout given in ticks or in seconds (rounded up to whole ticks)."""
     if ticks is not None and seconds is not None:
         raise ValueError("Specify ticks or seconds, not both")
     if seconds is not None:
-        if not math.isfinite(seconds) or seconds <= 0:
+        if not (math.isfinite(seconds) and seconds > 0):
             raise ValueError("Timeout seconds must be positive and finite")
         ticks = math.ceil(seconds * carl.PHYS_TICKS_PER_SECOND)
-    if ticks is not None and ticks < 1:
+    if ticks is None:
+        return default
+    if ticks < 1:
         raise ValueError("Timeout ticks must be positive")
-    return default if ticks is None else ticks
+    return ticks
 
 
-_OPTIONAL_FIELDS = ("car_boost", "car_internal_state", "blue_score", "orange_score", "episode_ticks")
+# ----------------------------------------------------------------- streams
 
+class _StreamBridge:
+    """Orders work between the caller's current torch stream and the
+    engine's stream: both wait for each other (or, with `synchronize`, the
+    whole device is synchronised)."""
+
+    def __init__(self, handle: int, device: th.device, synchronize: bool):
+        self.device = device
+        self.synchronize = synchronize
+        self.engine = th.cuda.ExternalStream(handle, device=device)
+
+    def join(self) -> None:
+        if self.synchronize:
+            th.cuda.synchronize(self.device)
+            return
+        caller = th.cuda.current_stream(self.device)
+        self.engine.wait_stream(caller)
+        caller.wait_stream(self.engine)
+
+
+# ------------------------------------------------------------------ resets
+
+_REQUIRED = ("ball_position", "ball_velocity", "ball_angular_velocity", "car_position", "car_rotation",
+             "car_velocity", "car_angular_velocity", "car_demoed")
+_OPTIONAL = ("car_boost", "car_internal_state", "blue_score", "orange_score", "episode_ticks")
+
+
+class _ResetRequest(NamedTuple):
+    """Arguments of one Env.apply_reset_state call."""
+    required: tuple[th.Tensor, ...]      # in _REQUIRED order
+    optional: dict[str, th.Tensor | None]
+    indices: th.Tensor | None
+    mask: th.Tensor | None
+
+
+def _contiguous(x: th.Tensor | None) -> th.Tensor | None:
+    return None if x is None else x.contiguous()
+
+
+def _arena_selection(mask: th.Tensor, eligible: th.Tensor) -> th.Tensor:
+    """A provider's mask restricted to the arenas eligible for a reset."""
+    if mask.shape != (len(eligible),) or mask.dtype != th.bool or mask.device != eligible.device:
+        raise ValueError("reset_mask must be bool [n_sim] on the environment device")
+    return (mask & eligible).contiguous()
+
+
+def _request_from_mapping(state: Mapping[str, th.Tensor], eligible: th.Tensor,
+                          masked_only: bool) -> _ResetRequest | None:
+    if "reset_mask" in state:
+        if "simulation_indices" in state:
+            raise ValueError("specify reset_mask or simulation_indices, not both")
+        indices, mask = None, _arena_selection(state["reset_mask"], eligible)
+    else:
+        if masked_only:
+            raise ValueError("masked reset providers must supply reset_mask")
+        indices = state.get("simulation_indices")
+        if indices is None:
+            indices = eligible.nonzero(as_tuple=True)[0]
+        if indices.numel() == 0:
+            return None
+        indices, mask = indices.contiguous(), None
+    return _ResetRequest(tuple(state[k].contiguous() for k in _REQUIRED),
+                         {k: _contiguous(state.get(k)) for k in _OPTIONAL}, indices, mask)
+
+
+def _request_from_typed(state: CARLResetState, eligible: th.Tensor, n_cars: int,
+                        masked_only: bool) -> _ResetRequest | None:
+    masked = state.reset_mask is not None
+    if masked_only and not masked:
+        raise ValueError("masked reset providers must supply reset_mask")
+    state.validate(eligible, n_cars)
+    if not masked and state.simulation_indices.numel() == 0:
+        return None
+    ball, cars = state.physical()
+    # fixed-shape requests stay on the device: no host-side rotation check
+    rotation = _forward_up_to_quat(cars.forward, cars.up, validate=not masked).contiguous()
+    required = (ball.position, ball.velocity, ball.angular_velocity, cars.position, rotation, cars.velocity,
+                cars.angular_velocity, cars.demoed)
+    match = state.match
+    optional = {
+        "car_boost": cars.boost,
+        "car_internal_state": state.car_internal_state,
+        "blue_score": None if match is None else match.blue_score,
+        "orange_score": None if match is None else match.orange_score,
+        "episode_ticks": None if match is None else match.episode_ticks,
+    }
+    return _ResetRequest(tuple(x.contiguous() for x in required), {k: _contiguous(v) for k, v in optional.items()},
+                         None if masked else state.simulation_indices.contiguous(),
+                         _arena_selection(state.reset_mask, eligible) if masked else None)
+
+
+# ---------------------------------------------------------------- episodes
+
+class _EpisodeLedger:
+    """Running return and length per agent, and the reports of episodes that
+    end: returned by the step that ends them, or (deferred) kept on the
+    device until drained, in step and agent order."""
+
+    def __init__(self, n_envs: int, device: th.device, deferred: bool):
+        self.deferred = deferred
+        self.returns = th.zeros(n_envs, device=device)
+        self.lengths = th.zeros(n_envs, dtype=th.int64, device=device)
+        self.pending: list[tuple[th.Tensor, th.Tensor, th.Tensor]] = []
+
+    def clear(self) -> None:
+        self.returns.zero_()
+        self.lengths.zero_()
+        self.pending.clear()
+
+    def record(self, reward: th.Tensor, done: th.Tensor) -> dict[str, list[Any]] | None:
+        """Add a step; the report of the episodes it ends (None if none
+        ended or reports are deferred)."""
+        self.returns += reward
+        self.lengths += 1
+        if self.deferred:
+            self.pending.append((self.returns.clone(), self.lengths.clone(), done.clone()))
+            self.returns.masked_fill_(done, 0)
+            self.lengths.masked_fill_(done, 0)
+            return None
+        ended = done.nonzero(as_tuple=True)[0]
+        if ended.numel() == 0:
+            return None
+        report = {"reward": self.returns[ended].cpu().tolist(), "length": self.lengths[ended].cpu().tolist()}
+        self.returns[ended] = 0
+        self.lengths[ended] = 0
+        return report
+
+    def drain(self) -> dict[str, list[Any]]:
+        if not self.pending:
+            return {"reward": [], "length": []}
+        returns, lengths, dones = (th.stack(x).flatten() for x in zip(*self.pending))
+        ended = dones.nonzero(as_tuple=True)[0]
+        self.pending.clear()
+        return {"reward": returns[ended].cpu().tolist(), "length": lengths[ended].cpu().tolist()}
+
+
+# ----------------------------------------------------------- environment
 
 class CARLTorchVectorEnv(VectorEnv):
-    """Torch vector environment with optional fixed-shape reset providers.
+    """Torch vector environment, one agent per car of every arena.
 
-    ``masked_resets=True`` calls the provider on every step, including when no
-    arena is done; it must return full-size tensors and ``reset_mask``.
-    Input storage must not be modified until the engine stream has read it.
+    With ``masked_resets=True`` the reset provider is called on every step,
+    also when no arena finished, and must return full-size tensors with a
+    ``reset_mask`` (CARLResetState or mapping); the selection stays on the
+    GPU.  Providers may return None.  Input storage must stay unchanged until
+    the engine's stream has read it.
     """
 
     metadata = {"render_modes": [], "autoreset_mode": AutoresetMode.SAME_STEP}
@@ -122,44 +285,47 @@ class CARLTorchVectorEnv(VectorEnv):
         super().__init__()
         if max_ticks < 1 or reward_scale <= 0:
             raise ValueError("max_ticks and reward_scale must be positive")
+        overtime = _ticks(overtime_timeout_ticks, overtime_timeout_seconds, REGULATION_TICKS)
+        no_touch = _ticks(no_touch_timeout_ticks, no_touch_timeout_seconds, 0)
 
-        self.n_sim = n_sim
         self.device = th.device("cuda:0")
         self.closed = False
-        self._seed = seed
-        self._copy_outputs = copy_outputs
-        self._synchronize = synchronize
         self.reward_funcs = list(reward_funcs or ())
         self.reward_scale = reward_scale
         self.reset_state_provider = reset_state_provider
         self.masked_resets = masked_resets
         self.defer_episode_reporting = defer_episode_reporting
-        self._episode_reports: list[tuple[th.Tensor, th.Tensor, th.Tensor]] = []
         self.discrete_actions = discrete_actions
-        self._state: CarlState | None = None
-        self._observation: CARLObservation | None = None
+        self._seed = seed
+        self._copy_outputs = copy_outputs
 
-        self._env = carl.Env(n_sim=n_sim, n_blue=n_blue, n_orange=n_orange, seed=seed, frameskip=frameskip,
-                             invert_orange=invert_orange, normalize=normalize, previous_controls=previous_controls)
-        self._stream = th.cuda.ExternalStream(self._env.stream, device=self.device)
-        self._env.max_ticks = max_ticks
-        self._env.overtime_timeout_ticks = _ticks(overtime_timeout_ticks, overtime_timeout_seconds, REGULATION_TICKS)
-        self._env.no_touch_timeout_ticks = _ticks(no_touch_timeout_ticks, no_touch_timeout_seconds, 0)
+        env = carl.Env(n_sim=n_sim, n_blue=n_blue, n_orange=n_orange, seed=seed, frameskip=frameskip,
+                       invert_orange=invert_orange, normalize=normalize, previous_controls=previous_controls)
+        env.max_ticks = max_ticks
+        env.overtime_timeout_ticks = overtime
+        env.no_touch_timeout_ticks = no_touch
+        self._env = env
+        self._bridge = _StreamBridge(env.stream, self.device, synchronize)
 
-        self.n_cars = self._env.n_cars
+        self.n_sim = n_sim
+        self.n_cars = env.n_cars
         self.n_envs = n_sim * self.n_cars
-        self._team_sign = th.tensor([1.0] * n_blue + [-1.0] * n_orange, dtype=th.float32, device=self.device)
-        self._boost_pad_positions = th.tensor(BOOST_PAD_POSITIONS, dtype=th.float32, device=self.device)
-        self.action_codec = (CARLActionCodec(previous_controls=previous_controls).to(self.device)
-                             if discrete_actions else None)
+        self._obs_dim = env.obs_dim
+        self._team_sign = th.tensor([1.0] * n_blue + [-1.0] * n_orange, device=self.device)
+        self._pad_positions = th.tensor(BOOST_PAD_POSITIONS, dtype=th.float32, device=self.device)
+        self.action_codec = CARLActionCodec(previous_controls).to(self.device) if discrete_actions else None
+        self._ledger = _EpisodeLedger(self.n_envs, self.device, defer_episode_reporting)
 
-        self._episode_return = th.zeros(self.n_envs, device=self.device)
-        self._episode_length = th.zeros(self.n_envs, dtype=th.int64, device=self.device)
+        # match state at the end of the last step (reward context), cleared
+        # for the arenas that reset
         self._score_difference = th.zeros(n_sim, dtype=th.int32, device=self.device)
         self._episode_ticks = th.zeros(n_sim, dtype=th.int32, device=self.device)
         self._overtime = th.zeros(n_sim, dtype=th.bool, device=self.device)
+        # state and observation after the last step or reset (reward context)
+        self._state: CarlState | None = None
+        self._observation: CARLObservation | None = None
 
-        self.single_observation_space = Box(-np.inf, np.inf, (self._env.obs_dim,), np.float32)
+        self.single_observation_space = Box(-np.inf, np.inf, (self._obs_dim,), np.float32)
         if discrete_actions:
             self.single_action_space = MultiDiscrete(np.asarray(carl.ACTION_NVECS, dtype=np.int64))
         else:
@@ -168,120 +334,62 @@ class CARLTorchVectorEnv(VectorEnv):
         self.observation_space = batch_space(self.single_observation_space, self.n_envs)
         self.action_space = batch_space(self.single_action_space, self.n_envs)
 
-    # ------------------------------------------------------------- plumbing
+    # -- native outputs
 
-    def _check_open(self) -> None:
-        if self.closed:
-            raise RuntimeError("Environment is closed")
-
-    def _sync(self) -> None:
-        if self._synchronize:
-            th.cuda.synchronize(self.device)
-            return
-        current = th.cuda.current_stream(self.device)
-        self._stream.wait_stream(current)
-        current.wait_stream(self._stream)
-
-    def _tensor(self, capsule: object, *, copy: bool | None = None) -> th.Tensor:
+    def _read(self, capsule: object, copy: bool | None = None) -> th.Tensor:
+        """An engine output as a tensor: a copy, or (copy_outputs=False) a
+        view that the engine rewrites on its next call."""
         x = th.from_dlpack(capsule)
         return x.clone() if (self._copy_outputs if copy is None else copy) else x
 
-    def _carl_state(self, capsule: object) -> CarlState:
-        return CarlState.from_raw(self._tensor(capsule, copy=True), self.n_cars, self._boost_pad_positions,
-                                  self._team_sign)
+    def _obs_view(self, capsule: object) -> CARLObservation:
+        return CARLObservation.from_tensor(self._read(capsule).view(self.n_envs, self._obs_dim), self.n_cars)
 
-    def _observation_of(self, capsule: object) -> CARLObservation:
-        return CARLObservation.from_tensor(self._tensor(capsule).view(self.n_envs, self._env.obs_dim), self.n_cars)
+    def _canonical(self, capsule: object) -> CarlState:
+        return CarlState.from_raw(self._read(capsule, copy=True), self.n_cars, self._pad_positions, self._team_sign)
 
     def _observe(self) -> CARLObservation:
-        self._sync()
-        observation = self._observation_of(self._env.get_obs())
-        self._state = self._carl_state(self._env.get_state()) if self.reward_funcs else None
-        self._observation = observation if self.reward_funcs else None
-        return observation
+        self._bridge.join()
+        obs = self._obs_view(self._env.get_obs())
+        keep = bool(self.reward_funcs)
+        self._state = self._canonical(self._env.get_state()) if keep else None
+        self._observation = obs if keep else None
+        return obs
 
-    def _per_car(self, x: th.Tensor) -> th.Tensor:
-        return x[:, None].expand(-1, self.n_cars).reshape(self.n_envs)
+    def _agents(self, per_arena: th.Tensor) -> th.Tensor:
+        """[n_sim] -> [n_envs], one entry per car."""
+        return per_arena.repeat_interleave(self.n_cars)
 
-    # ---------------------------------------------------------- reset states
+    def _ensure_open(self) -> None:
+        if self.closed:
+            raise RuntimeError("Environment is closed")
 
-    def _reset_selection(self, mask: th.Tensor, eligible: th.Tensor) -> th.Tensor:
-        if mask.shape != (self.n_sim,) or mask.dtype != th.bool or mask.device != eligible.device:
-            raise ValueError("reset_mask must be bool [n_sim] on the environment device")
-        return (mask & eligible).contiguous()
+    # -- resets
 
     def _apply_reset_state(self, reset_mask: th.Tensor) -> None:
-        if self.reset_state_provider is None:
+        """Run the reset provider for the arenas in `reset_mask` (bool
+        [n_sim]) and apply what it returns."""
+        provider = self.reset_state_provider
+        if provider is None or not (self.masked_resets or reset_mask.any()):
             return
-        if not self.masked_resets and not reset_mask.any():
-            return
-        state = self.reset_state_provider(reset_mask)
+        state = provider(reset_mask)
         if state is None:
             return
         if isinstance(state, CARLResetState):
-            self._apply_typed_reset_state(state, reset_mask)
+            request = _request_from_typed(state, reset_mask, self.n_cars, self.masked_resets)
         else:
-            self._apply_mapping_reset_state(state, reset_mask)
-
-    def _apply_mapping_reset_state(self, state: Mapping[str, th.Tensor], reset_mask: th.Tensor) -> None:
-        indices = mask = None
-        if "reset_mask" in state:
-            if "simulation_indices" in state:
-                raise ValueError("specify reset_mask or simulation_indices, not both")
-            mask = self._reset_selection(state["reset_mask"], reset_mask)
-        else:
-            if self.masked_resets:
-                raise ValueError("masked reset providers must supply reset_mask")
-            indices = state.get("simulation_indices")
-            if indices is None:
-                indices = reset_mask.nonzero(as_tuple=True)[0]
-            if not indices.numel():
-                return
-            indices = indices.contiguous()
-        optional = {k: (state[k].contiguous() if k in state else None) for k in _OPTIONAL_FIELDS}
-        self._env.apply_reset_state(
-            state["ball_position"].contiguous(), state["ball_velocity"].contiguous(),
-            state["ball_angular_velocity"].contiguous(), state["car_position"].contiguous(),
-            state["car_rotation"].contiguous(), state["car_velocity"].contiguous(),
-            state["car_angular_velocity"].contiguous(), state["car_demoed"].contiguous(),
-            **optional, simulation_indices=indices, reset_mask=mask)
-
-    def _apply_typed_reset_state(self, state: CARLResetState, reset_mask: th.Tensor) -> None:
-        masked = state.reset_mask is not None
-        if self.masked_resets and not masked:
-            raise ValueError("masked reset providers must supply reset_mask")
-        state.validate(reset_mask, self.n_cars)
-        if not masked and not state.simulation_indices.numel():
+            request = _request_from_mapping(state, reset_mask, self.masked_resets)
+        if request is None:
             return
-        ball, cars = state.physical()
-        rotation = _forward_up_to_quat(cars.forward, cars.up, validate=not masked).contiguous()
-        match = state.match
-        self._env.apply_reset_state(
-            ball.position.contiguous(), ball.velocity.contiguous(), ball.angular_velocity.contiguous(),
-            cars.position.contiguous(), rotation, cars.velocity.contiguous(), cars.angular_velocity.contiguous(),
-            cars.demoed.contiguous(), car_boost=cars.boost.contiguous(),
-            car_internal_state=(state.car_internal_state.contiguous()
-                                if state.car_internal_state is not None else None),
-            blue_score=match.blue_score.contiguous() if match is not None else None,
-            orange_score=match.orange_score.contiguous() if match is not None else None,
-            episode_ticks=match.episode_ticks.contiguous() if match is not None else None,
-            simulation_indices=None if masked else state.simulation_indices.contiguous(),
-            reset_mask=self._reset_selection(state.reset_mask, reset_mask) if masked else None)
+        self._env.apply_reset_state(*request.required, **request.optional,
+                                    simulation_indices=request.indices, reset_mask=request.mask)
 
-    def _clear_sim_stats(self, mask: th.Tensor | None = None) -> None:
-        if mask is None:
-            self._episode_reports.clear()
-            self._episode_return.zero_()
-            self._episode_length.zero_()
-            self._score_difference.zero_()
-            self._episode_ticks.zero_()
-            self._overtime.zero_()
-            return
-        self._score_difference.masked_fill_(mask, 0)
-        self._episode_ticks.masked_fill_(mask, 0)
-        self._overtime.masked_fill_(mask, False)
+    def _forget_match(self, arenas: th.Tensor) -> None:
+        self._score_difference.masked_fill_(arenas, 0)
+        self._episode_ticks.masked_fill_(arenas, 0)
+        self._overtime.masked_fill_(arenas, False)
 
-    # -------------------------------------------------------------- rewards
+    # -- rewards
 
     def register_reward(self, reward_function: RewardFunction) -> RewardFunction:
         self.reward_funcs.append(reward_function)
@@ -292,141 +400,118 @@ class CARLTorchVectorEnv(VectorEnv):
             raise RuntimeError("continuous controls do not use a categorical action mask")
         return self.action_codec.mask(observation)
 
-    def _custom_reward(self, actions, score_delta, done, terminated, truncated):
+    def _reward_context(self, actions: th.Tensor, events: CarlEvents) -> RewardContext:
         if self._state is None or self._observation is None:
             raise RuntimeError("reset must be called before using custom rewards")
-        context = RewardContext(
-            current=self._carl_state(self._env.get_transition_state()),
+        return RewardContext(
+            current=self._canonical(self._env.get_transition_state()),
             previous=self._state,
-            current_observation=self._observation_of(self._env.get_obs()),
+            current_observation=self._obs_view(self._env.get_obs()),
             previous_observation=self._observation,
-            events=CarlEvents(score_delta=score_delta, done=done, terminated=terminated, truncated=truncated),
+            events=events,
             actions=actions,
             score_difference=self._score_difference,
             episode_ticks=self._episode_ticks,
             overtime=self._overtime,
         )
-        reward = th.zeros((self.n_sim, self.n_cars), device=self.device)
+
+    def _custom_reward(self, actions: th.Tensor, events: CarlEvents) -> tuple[th.Tensor, dict[str, list[Any]]]:
+        context = self._reward_context(actions, events)
+        total = th.zeros((self.n_sim, self.n_cars), device=self.device)
         info: dict[str, list[Any]] = {}
         for func in self.reward_funcs:
-            result = func(context)
-            if isinstance(result, RewardResult):
-                info.update(result.info)
-                result = result.reward
-            if result.shape != reward.shape:
-                raise ValueError(f"Reward must have shape {tuple(reward.shape)}")
-            reward += result
-        return (reward * self.reward_scale).reshape(self.n_envs), info
+            out = func(context)
+            if isinstance(out, RewardResult):
+                info.update(out.info)
+                out = out.reward
+            if out.shape != total.shape:
+                raise ValueError(f"Reward must have shape {tuple(total.shape)}")
+            total += out
+        return (total * self.reward_scale).reshape(self.n_envs), info
 
-    # ------------------------------------------------------------ gym API
+    # -- gymnasium API
 
     def reset(self, *, seed: int | None = None, options: dict[str, Any] | None = None) -> th.Tensor:
-        self._check_open()
+        self._ensure_open()
         if seed is not None and seed != self._seed:
             raise ValueError("CARL's seed is constructor-only")
         if options:
             raise NotImplementedError("CARL reset options are not supported")
-        self._sync()
+        self._bridge.join()
         self._env.reset()
         self._apply_reset_state(th.ones(self.n_sim, dtype=th.bool, device=self.device))
-        self._clear_sim_stats()
+        self._ledger.clear()
+        for x in (self._score_difference, self._episode_ticks, self._overtime):
+            x.zero_()
         return self._observe()
 
-    def set_ball(self, position, velocity, angular_velocity, *, simulation_indices=None) -> th.Tensor:
-        self._check_open()
-        self._sync()
+    def set_ball(self, position: th.Tensor, velocity: th.Tensor, angular_velocity: th.Tensor, *,
+                 simulation_indices: th.Tensor | None = None) -> th.Tensor:
+        self._ensure_open()
+        self._bridge.join()
         self._env.set_ball(position.contiguous(), velocity.contiguous(), angular_velocity.contiguous(),
-                           simulation_indices=(simulation_indices.contiguous()
-                                               if simulation_indices is not None else None))
+                           simulation_indices=_contiguous(simulation_indices))
         return self._observe()
 
-    def set_car(self, position, rotation, velocity, angular_velocity, demoed, *, boost=None, internal_state=None,
-                simulation_indices=None) -> th.Tensor:
-        self._check_open()
-        self._sync()
+    def set_car(self, position: th.Tensor, rotation: th.Tensor, velocity: th.Tensor, angular_velocity: th.Tensor,
+                demoed: th.Tensor, *, boost: th.Tensor | None = None, internal_state: th.Tensor | None = None,
+                simulation_indices: th.Tensor | None = None) -> th.Tensor:
+        self._ensure_open()
+        self._bridge.join()
         self._env.set_car(position.contiguous(), rotation.contiguous(), velocity.contiguous(),
-                          angular_velocity.contiguous(), demoed.contiguous(),
-                          boost=boost.contiguous() if boost is not None else None,
-                          internal_state=internal_state.contiguous() if internal_state is not None else None,
-                          simulation_indices=(simulation_indices.contiguous()
-                                              if simulation_indices is not None else None))
+                          angular_velocity.contiguous(), demoed.contiguous(), boost=_contiguous(boost),
+                          internal_state=_contiguous(internal_state),
+                          simulation_indices=_contiguous(simulation_indices))
         return self._observe()
 
-    def step(self, actions):
-        self._check_open()
-        dtype = th.int32 if self.discrete_actions else th.float32
-        actions = th.as_tensor(actions, dtype=dtype, device=self.device).contiguous()
+    def step(self, actions: th.Tensor | np.ndarray):
+        self._ensure_open()
         width = len(carl.ACTION_NVECS)
+        actions = th.as_tensor(actions, dtype=th.int32 if self.discrete_actions else th.float32,
+                               device=self.device).contiguous()
         if actions.shape != (self.n_envs, width):
             raise ValueError(f"Expected actions shaped {(self.n_envs, width)}")
         actions = actions.view(self.n_sim, self.n_cars, width)
 
-        self._sync()
-        if self.discrete_actions:
-            self._env.step(actions)
-        else:
-            self._env.step_continuous(actions)
-        self._sync()
+        self._bridge.join()
+        (self._env.step if self.discrete_actions else self._env.step_continuous)(actions)
+        self._bridge.join()
 
-        score_delta = self._tensor(self._env.get_rewards())
-        sim_done = self._tensor(self._env.get_dones())
-        self._score_difference = self._tensor(self._env.get_transition_score_difference())
-        self._episode_ticks = self._tensor(self._env.get_transition_episode_ticks())
-        self._overtime = self._tensor(self._env.get_transition_overtime())
-        sim_terminated = sim_done & score_delta.ne(0)
-        sim_truncated = sim_done & ~sim_terminated
+        env = self._env
+        score_delta = self._read(env.get_rewards())
+        finished = self._read(env.get_dones())
+        self._score_difference = self._read(env.get_transition_score_difference())
+        self._episode_ticks = self._read(env.get_transition_episode_ticks())
+        self._overtime = self._read(env.get_transition_overtime())
+        goal = finished & (score_delta != 0)
+        events = CarlEvents(score_delta=score_delta, done=finished, terminated=goal, truncated=finished & ~goal)
 
         if self.reward_funcs:
-            reward, reward_info = self._custom_reward(actions, score_delta, sim_done, sim_terminated, sim_truncated)
+            reward, reward_info = self._custom_reward(actions, events)
         else:
-            reward = (score_delta[:, None] * self._team_sign).reshape(self.n_envs)
-            reward_info = {}
+            reward, reward_info = (score_delta[:, None] * self._team_sign).reshape(self.n_envs), {}
 
-        self._apply_reset_state(sim_done)
-        self._clear_sim_stats(sim_done)
+        self._apply_reset_state(finished)
+        self._forget_match(finished)
         obs = self._observe()
 
-        terminated = self._per_car(sim_terminated)
-        truncated = self._per_car(sim_truncated)
+        terminated, truncated = self._agents(events.terminated), self._agents(events.truncated)
         done = terminated | truncated
-        self._episode_return += reward
-        self._episode_length += 1
-
+        report = self._ledger.record(reward, done)
         if self.defer_episode_reporting:
-            self._episode_reports.append((self._episode_return.clone(), self._episode_length.clone(), done.clone()))
-            self._episode_return.masked_fill_(done, 0)
-            self._episode_length.masked_fill_(done, 0)
-            info = {**reward_info, "final_obs": self._observation_of(self._env.get_transition_obs()),
-                    "_final_obs": done}
-            return obs, reward, terminated, truncated, info
-
-        finished = done.nonzero(as_tuple=True)[0]
-        info: dict[str, Any] = {"reward": [], "length": []}
-        if finished.numel():
-            info = {
-                "reward": self._episode_return[finished].cpu().tolist(),
-                "length": self._episode_length[finished].cpu().tolist(),
-                "final_obs": self._observation_of(self._env.get_transition_obs()),
-                "_final_obs": done,
-                **reward_info,
-            }
-            self._episode_return[finished] = 0
-            self._episode_length[finished] = 0
+            info = {**reward_info, "final_obs": self._obs_view(env.get_transition_obs()), "_final_obs": done}
+        elif report is None:
+            info = {"reward": [], "length": []}
+        else:
+            info = {**report, "final_obs": self._obs_view(env.get_transition_obs()), "_final_obs": done,
+                    **reward_info}
         return obs, reward, terminated, truncated, info
 
     def drain_episode_reports(self) -> dict[str, list[Any]]:
-        """Completed episodes since the last drain, in step then actor order."""
-        self._check_open()
-        if not self._episode_reports:
-            return {"reward": [], "length": []}
-        returns, lengths, dones = zip(*self._episode_reports)
-        finished = th.stack(dones).flatten().nonzero(as_tuple=True)[0]
-        reports = {
-            "reward": th.stack(returns).flatten()[finished].cpu().tolist(),
-            "length": th.stack(lengths).flatten()[finished].cpu().tolist(),
-        }
-        self._episode_reports.clear()
-        return reports
+        """Reports of every episode that ended since the last drain, in step
+        and agent order (deferred reporting).  reset() discards them."""
+        self._ensure_open()
+        return self._ledger.drain()
 
     def render(self) -> None:
         return None
@@ -434,9 +519,6 @@ class CARLTorchVectorEnv(VectorEnv):
     def close(self, **_: Any) -> None:
         if self.closed:
             return
-        self._sync()
+        self._bridge.join()
         del self._env
         self.closed = True
-
-
-__all__ = ["CARLTorchVectorEnv", "ResetStateProvider", "RewardFunction"]

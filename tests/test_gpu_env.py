@@ -15,9 +15,10 @@ import pytest
 import torch
 
 import carl
-from carl.gymnasium.state import CARLBall, CARLCars, CARLMatchReset, CARLObservation, CARLResetState
+from carl.gymnasium.state import CARLObservation
 from carl.gymnasium.torch import CARLTorchVectorEnv
-from test_python_layer import FixedShapeOnly
+import reset_fixtures as fixtures
+from reset_fixtures import NoHostSync, typed_reset_state
 
 pytestmark = pytest.mark.gpu
 
@@ -38,34 +39,7 @@ def check_tensor(value, shape, dtype):
 
 
 def reset_inputs(n, n_cars, *, match=True, internal=True, device="cuda"):
-    """tests/test_resets.py:28-72 inputs."""
-    ball_position = zeros(n, 3, device=device)
-    ball_position[:, 2] = 800
-    ball_velocity = zeros(n, 3, device=device)
-    ball_velocity[:, 0] = 170
-    car_position = zeros(n, n_cars, 3, device=device)
-    car_position[..., 0] = torch.arange(n_cars, device=device) * 250 - 500
-    car_position[..., 1] = -1000
-    car_position[..., 2] = 17
-    car_rotation = zeros(n, n_cars, 4, device=device)
-    car_rotation[..., 3] = 1
-    demoed = torch.zeros((n, n_cars), device=device, dtype=torch.bool)
-    demoed[:, -1] = True
-    out = {"ball_position": ball_position, "ball_velocity": ball_velocity,
-           "ball_angular_velocity": zeros(n, 3, device=device), "car_position": car_position,
-           "car_rotation": car_rotation, "car_velocity": zeros(n, n_cars, 3, device=device),
-           "car_angular_velocity": zeros(n, n_cars, 3, device=device), "car_demoed": demoed,
-           "car_boost": zeros(n, n_cars, device=device).fill_(61)}
-    if internal:
-        values = zeros(n, n_cars, carl.CAR_INTERNAL_SIZE, device=device)
-        values[..., 3] = 1
-        values[..., 5] = 1
-        out["car_internal_state"] = values
-    if match:
-        out.update(blue_score=torch.full((n,), 2, device=device, dtype=torch.int32),
-                   orange_score=torch.full((n,), 1, device=device, dtype=torch.int32),
-                   episode_ticks=torch.full((n,), 23, device=device, dtype=torch.int32))
-    return out
+    return fixtures.reset_inputs(n, n_cars, match=match, internal=internal, device=device)
 
 
 def sequential_reset(env, values, indices):
@@ -78,20 +52,6 @@ def sequential_reset(env, values, indices):
     if "blue_score" in values:
         env.set_match_state(values["blue_score"], values["orange_score"], values["episode_ticks"],
                             simulation_indices=indices)
-
-
-def typed_reset_state(values, indices=None, *, reset_mask=None):
-    ball = CARLBall.from_tensor(torch.cat((values["ball_position"], values["ball_velocity"],
-                                           values["ball_angular_velocity"]), dim=-1))
-    count, n_cars = values["car_position"].shape[:2]
-    cars = CARLCars.from_tensor(zeros(count, n_cars, carl.OBS_PER_CAR, device=values["car_position"].device), n_cars)
-    cars.position.copy_(values["car_position"])
-    cars.forward[..., 0] = 1
-    cars.up[..., 2] = 1
-    cars.boost.copy_(values["car_boost"])
-    cars[..., carl.OBS_DEMOED] = values["car_demoed"]
-    match = CARLMatchReset(values["blue_score"], values["orange_score"], values["episode_ticks"])
-    return CARLResetState(indices, ball, cars, values["car_internal_state"], match, reset_mask=reset_mask)
 
 
 def reset_provider(mask, *, typed, masked=False):
@@ -424,7 +384,7 @@ def test_deferred_episode_reports_match_immediate_reports(gpu, copy_outputs):
     expected = {"reward": [], "length": []}
     for _ in range(5):
         control = reference.step(actions)
-        with FixedShapeOnly():
+        with NoHostSync():
             actual = env.step(actions)
         for a, e in zip(actual[:4], control[:4]):
             assert_same(a, e)

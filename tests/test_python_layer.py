@@ -13,11 +13,11 @@ from unittest import mock
 
 import pytest
 import torch
-from torch.utils._python_dispatch import TorchDispatchMode
 
 import carl
-from carl.gymnasium.state import CARLBall, CARLCar, CARLCars, CARLMatchReset, CARLResetState
+from carl.gymnasium.state import CARLBall, CARLCar, CARLCars
 from carl.gymnasium.torch import CARLTorchVectorEnv
+from reset_fixtures import NoHostSync, reset_inputs, typed_reset_state
 
 
 # ------------------------------------------------------------------ state views
@@ -51,77 +51,12 @@ def test_cars_inherit_car_fields_and_ego():
 
 # ------------------------------------------------------------------ reset dispatch
 
-def _zeros(*shape):
-    return torch.zeros(shape, dtype=torch.float32)
-
-
-def reset_inputs(n_selected, n_cars, *, match=True, internal=True):
-    ball_position = _zeros(n_selected, 3)
-    ball_position[:, 2] = 800
-    ball_velocity = _zeros(n_selected, 3)
-    ball_velocity[:, 0] = 170
-    car_position = _zeros(n_selected, n_cars, 3)
-    car_position[..., 0] = torch.arange(n_cars) * 250 - 500
-    car_position[..., 1] = -1000
-    car_position[..., 2] = 17
-    car_rotation = _zeros(n_selected, n_cars, 4)
-    car_rotation[..., 3] = 1
-    demoed = torch.zeros((n_selected, n_cars), dtype=torch.bool)
-    demoed[:, -1] = True
-    out = {
-        "ball_position": ball_position, "ball_velocity": ball_velocity,
-        "ball_angular_velocity": _zeros(n_selected, 3), "car_position": car_position,
-        "car_rotation": car_rotation, "car_velocity": _zeros(n_selected, n_cars, 3),
-        "car_angular_velocity": _zeros(n_selected, n_cars, 3), "car_demoed": demoed,
-        "car_boost": _zeros(n_selected, n_cars).fill_(61),
-    }
-    if internal:
-        values = _zeros(n_selected, n_cars, carl.CAR_INTERNAL_SIZE)
-        values[..., 3] = 1
-        values[..., 5] = 1
-        out["car_internal_state"] = values
-    if match:
-        out.update(blue_score=torch.full((n_selected,), 2, dtype=torch.int32),
-                   orange_score=torch.full((n_selected,), 1, dtype=torch.int32),
-                   episode_ticks=torch.full((n_selected,), 23, dtype=torch.int32))
-    return out
-
-
-def typed_reset_state(values, indices=None, *, reset_mask=None):
-    ball = CARLBall.from_tensor(torch.cat((values["ball_position"], values["ball_velocity"],
-                                           values["ball_angular_velocity"]), dim=-1))
-    count, n_cars = values["car_position"].shape[:2]
-    cars = CARLCars.from_tensor(_zeros(count, n_cars, carl.OBS_PER_CAR), n_cars)
-    cars.position.copy_(values["car_position"])
-    cars.forward[..., 0] = 1
-    cars.up[..., 2] = 1
-    cars.boost.copy_(values["car_boost"])
-    cars[..., carl.OBS_DEMOED] = values["car_demoed"]
-    match = CARLMatchReset(values["blue_score"], values["orange_score"], values["episode_ticks"])
-    return CARLResetState(ball=ball, cars=cars, match=match, simulation_indices=indices, reset_mask=reset_mask,
-                          car_internal_state=values.get("car_internal_state"))
-
-
 def reset_provider(mask, *, typed):
     indices = mask.nonzero().flatten()
     values = reset_inputs(len(indices), 2)
     if not typed:
         return values | {"simulation_indices": indices}
     return typed_reset_state(values, indices)
-
-
-class FixedShapeOnly(TorchDispatchMode):
-    """Fail on scalar readback or dynamic compaction in the masked wrapper path."""
-
-    def __torch_dispatch__(self, func, types, args=(), kwargs=None):
-        forbidden = (torch.ops.aten._local_scalar_dense.default, torch.ops.aten.nonzero.default,
-                     torch.ops.aten.masked_select.default, torch.ops.aten._unique2.default)
-        if func in forbidden:
-            raise AssertionError(f"host-dependent reset operation: {func}")
-        if func == torch.ops.aten.index.Tensor:
-            if any(i is not None and i.dtype in (torch.bool, torch.uint8) for i in args[1]):
-                raise AssertionError("boolean reset compaction")
-        return func(*args, **(kwargs or {}))
 
 
 def make_env(provider, masked=True):
@@ -143,7 +78,7 @@ def test_masked_provider_never_compacts_or_reads_scalars(typed, eligible):
     state = typed_reset_state(values, reset_mask=mask) if typed else values | {"reset_mask": mask}
     provider = mock.Mock(return_value=state)
     env = make_env(provider)
-    with FixedShapeOnly():
+    with NoHostSync():
         env._apply_reset_state(eligible)
     provider.assert_called_once_with(eligible)
     env._env.apply_reset_state.assert_called_once()
@@ -169,7 +104,7 @@ def test_masked_provider_validates_selection_metadata(typed, selection):
     else:
         state = values | selection
     env = make_env(mock.Mock(return_value=state))
-    with FixedShapeOnly(), pytest.raises(ValueError):
+    with NoHostSync(), pytest.raises(ValueError):
         env._apply_reset_state(torch.ones(3, dtype=torch.bool))
     env._env.apply_reset_state.assert_not_called()
 
@@ -187,7 +122,7 @@ def test_normalized_masked_inputs_remain_fixed_shape():
     state.cars.angular_velocity.div_(carl.CAR_MAX_ANG_SPEED)
     state.cars.boost.div_(carl.BOOST_MAX)
     env = make_env(mock.Mock(return_value=state))
-    with FixedShapeOnly():
+    with NoHostSync():
         env._apply_reset_state(mask)
     args, kwargs = env._env.apply_reset_state.call_args
     torch.testing.assert_close(args[0], values["ball_position"])
