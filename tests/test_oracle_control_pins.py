@@ -379,3 +379,117 @@ def test_reverse_throttle_follows_the_drive_curve():
     accel = np.diff(v)[3:] / DT
     np.testing.assert_allclose(accel, [1600.0 * _drive_curve(x) for x in v[2:-2]], rtol=0.02, atol=8.0)
     s.close()
+
+
+# ------------------------------------------------------------------ steering
+
+WHEELBASE = 37.3743 + 47.6257      # front and rear suspension x (include/RLConstants.cuh:84-87)
+_STEER_CURVE = ((0.0, 0.53356), (500.0, 0.31930), (1000.0, 0.18203), (1500.0, 0.10570), (1750.0, 0.08507),
+                (3000.0, 0.03454))
+
+
+def _steer_angle(speed: float) -> float:
+    """Published front-wheel steer angle at full lock (RLConstants.cuh:252-262)."""
+    pts = _STEER_CURVE
+    if speed <= 0.0:
+        return pts[0][1]
+    for (a, fa), (b, fb) in zip(pts, pts[1:]):
+        if speed <= b:
+            return fa + (fb - fa) * (speed - a) / (b - a)
+    return pts[-1][1]
+
+
+@pytest.mark.parametrize("target", [250.0, 300.0, 400.0])
+@pytest.mark.parametrize("steer", [1.0, -1.0])
+def test_full_lock_turning_radius_at_low_speed(target, steer):
+    """Held at a steady low speed with full lock, the car turns on the
+    circle of the kinematic bicycle model: yaw rate / speed = tan(delta) / L
+    with delta the published steer angle at that speed and L the distance
+    between the axles (lateral slip is negligible this slowly)."""
+    s = _settled_car(ALONG_Y, (0.0, -2000.0, 17.0))
+    kappa = []
+    for t in range(720):
+        v = s.car_vec("CARL_CAR_VEL", 0)
+        speed = float(np.hypot(v[0], v[1]))
+        throttle = float(np.clip((target - speed) / 100.0, -1.0, 1.0))
+        tick_direct(s, direct(throttle=throttle, steer=steer if t >= 60 else 0.0))
+        if t >= 600:
+            w = s.car_vec("CARL_CAR_ANG", 0)
+            kappa.append((w[2] / speed, speed))
+    got, speed = np.mean([k for k, _ in kappa]), np.mean([v for _, v in kappa])
+    assert abs(speed - target) < 0.05 * target
+    want = math.copysign(math.tan(_steer_angle(speed)) / WHEELBASE, steer)
+    assert abs(got / want - 1.0) < 0.02, (got, want, speed)
+    s.close()
+
+
+# ------------------------------------------------------------------ autoroll
+
+AUTOROLL_FORCE, AUTOROLL_TORQUE = 100.0, 80.0     # CAR_AUTOROLL_FORCE / _TORQUE (RLConstants.cuh:145-146)
+
+
+def _autoroll_difference(q, z):
+    """One tick from the same pose with a small throttle and with none; the
+    throttle's only same-tick effects are the autoroll and (off the ground)
+    the air throttle (drive and brake act a tick later)."""
+    s = Scene(1, 0)
+    s.place([[0.0, -1500.0, z]], [q], [[0.0, 0.0, 0.0]], [[0.0, 0.0, 0.0]])
+    saved = s.env.export_state()
+    out = []
+    for throttle in (0.0, 0.01):
+        s.env.import_state(*saved)
+        tick_direct(s, direct(throttle=throttle))
+        out.append((s.car_vec("CARL_CAR_VEL", 0), s.car_vec("CARL_CAR_ANG", 0)))
+        car, _, _ = s.env.export_state()
+        contacts = car[CAR["CARL_CAR_WHEEL_CONTACT_0"]:CAR["CARL_CAR_WHEEL_CONTACT_0"] + 4, 0].tolist()
+        chassis = int(car[CAR["CARL_CAR_MANIFOLD_COUNT"], 0])
+    s.close()
+    return out[1][0] - out[0][0], out[1][1] - out[0][1], contacts, chassis
+
+
+@pytest.mark.parametrize("phi,z,wheels", [(0.3, 28.0, [0, 1, 0, 1]), (0.6, 32.0, [0, 1, 0, 1]),
+                                          (-0.5, 28.0, [1, 0, 1, 0])])
+def test_autoroll_on_two_side_wheels_rolls_the_car_upright(phi, z, wheels):
+    """A car rolled by phi, on the two wheels of one side on the flat floor,
+    with throttle: autoroll pushes it down at CAR_AUTOROLL_FORCE and turns
+    it back about its nose: the contact-aligned right axis (floor normal x
+    nose) makes an angle phi with the car's right axis, so the torque is
+    CAR_AUTOROLL_TORQUE x (1 - cos phi), against the roll."""
+    q = quat_axis_angle((1, 0, 0), phi)
+    dv, dw, contacts, chassis = _autoroll_difference(q, z)
+    assert contacts == wheels and chassis == 0
+    nose = rot_matrix(q)[:, 0]
+    np.testing.assert_allclose(dv, [0.0, 0.0, -AUTOROLL_FORCE * DT] + nose * 0.01 * 200.0 / 3.0 * DT, atol=2e-5)
+    want = -math.copysign(1.0, phi) * np.array([1.0, 0.0, 0.0]) * (1.0 - math.cos(phi)) * AUTOROLL_TORQUE * DT
+    np.testing.assert_allclose(dw, want, atol=2e-6)
+
+
+@pytest.mark.parametrize("theta,z,wheels", [(0.25, 28.0, [1, 1, 0, 0]), (0.4, 36.0, [1, 1, 0, 0]),
+                                            (-0.35, 28.0, [0, 0, 1, 1])])
+def test_autoroll_on_two_end_wheels_pitches_the_car_level(theta, z, wheels):
+    """Pitched by theta onto its front (or rear) wheels: the pitch torque is
+    CAR_AUTOROLL_TORQUE x sin^2 theta about the car's right axis, against
+    the pitch (the nose projected on the floor-aligned frame keeps
+    cos^2 theta of it), plus (1 - cos theta) about the nose."""
+    q = quat_axis_angle((0, 1, 0), theta)
+    dv, dw, contacts, chassis = _autoroll_difference(q, z)
+    assert contacts == wheels and chassis == 0
+    r = rot_matrix(q)
+    nose, right = r[:, 0], r[:, 1]
+    np.testing.assert_allclose(dv, [0.0, 0.0, -AUTOROLL_FORCE * DT] + nose * 0.01 * 200.0 / 3.0 * DT, atol=2e-5)
+    pitch_back = -math.copysign(1.0, theta) * right * math.sin(theta) ** 2
+    want = (pitch_back - nose * (1.0 - math.cos(theta))) * AUTOROLL_TORQUE * DT
+    np.testing.assert_allclose(dw, want, atol=2e-6)
+
+
+def test_no_autoroll_on_four_wheels():
+    s = _settled_car()
+    saved = s.env.export_state()
+    out = []
+    for throttle in (0.0, 0.01):
+        s.env.import_state(*saved)
+        tick_direct(s, direct(throttle=throttle))
+        out.append((s.car_vec("CARL_CAR_VEL", 0), s.car_vec("CARL_CAR_ANG", 0)))
+    np.testing.assert_allclose(out[1][0], out[0][0], atol=1e-6)
+    np.testing.assert_allclose(out[1][1], out[0][1], atol=1e-7)
+    s.close()
