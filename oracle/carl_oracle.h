@@ -80,6 +80,12 @@ void oracle_probe_steer_stage(float staged, float* prev_out, float* cur_out);
 int oracle_kickoff_perm(int idx, int slot);
 /* SAT probes: triangle in box-local coordinates; two car hitboxes in world */
 void oracle_probe_box_tri_sat(const float* tri, int* overlap, int* axis_idx, float* depth, float* axis);
+int oracle_probe_box_tri_contacts(const float* tri, int* axis_idx, float* car_pos, float* arena_pos, float* normal,
+                                  float* depth);
+/* arena manifold of one car from the environment's current state */
+int oracle_probe_manifold(OEnv* env, int car, float* car_pos, float* world_pos, float* normal, float* dist);
+int oracle_probe_box_box_contacts(const float* cen_a, const float* rot_a, const float* cen_b, const float* rot_b,
+                                  int* axis_idx, float* car_pos_a, float* car_pos_b, float* normal, float* depth);
 void oracle_probe_box_box_sat(const float* cen_a, const float* rot_a, const float* cen_b, const float* rot_b,
                               int* overlap, int* axis_idx, float* depth);
 uint32_t oracle_hash32(uint32_t v);

@@ -783,6 +783,20 @@ void oracle_probe_autoflip(const float* q, int j, int n, const float* nrm, int* 
 void oracle_probe_steer_stage(float s, float* p, float* c) { ophys_probe_steer_stage(s, p, c); }
 int oracle_kickoff_perm(int i, int s) { return ophys_kickoff_perm(i, s); }
 void oracle_probe_box_tri_sat(const float* t, int* o, int* a, float* d, float* ax) { ophys_probe_box_tri_sat(t, o, a, d, ax); }
+int oracle_probe_box_tri_contacts(const float* t, int* a, float* cp, float* ap, float* n, float* d)
+{
+    return ophys_probe_box_tri_contacts(t, a, cp, ap, n, d);
+}
+int oracle_probe_manifold(OEnv* e, int car, float* cp, float* wp, float* n, float* d)
+{
+    if (car < 0 || car >= e->w.nTotal) return -1;
+    return ophys_probe_manifold(&e->w, car, cp, wp, n, d);
+}
+int oracle_probe_box_box_contacts(const float* ca, const float* ra, const float* cb, const float* rb, int* a,
+                                  float* pa, float* pb, float* n, float* d)
+{
+    return ophys_probe_box_box_contacts(ca, ra, cb, rb, a, pa, pb, n, d);
+}
 void oracle_probe_box_box_sat(const float* ca, const float* ra, const float* cb, const float* rb, int* o, int* a,
                               float* d)
 {

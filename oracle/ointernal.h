@@ -311,6 +311,11 @@ Q4 ophys_integrate_quat(Q4 rot, V3 ang);
 void ophys_controls_decode(int kind, const void* actions, int car, OControls* out);
 int ophys_kickoff_perm(int idx, int slot);
 void ophys_probe_box_tri_sat(const float* tri, int* overlap, int* axisIdx, float* depth, float* axis);
+int ophys_probe_box_tri_contacts(const float* tri, int* axisIdx, float* carPos, float* arenaPos, float* normal,
+                                 float* depth);
+int ophys_probe_manifold(OWorld* w, int ci, float* carPos, float* worldPos, float* normal, float* dist);
+int ophys_probe_box_box_contacts(const float* cenA, const float* rotA, const float* cenB, const float* rotB,
+                                 int* axisIdx, float* carPosA, float* carPosB, float* normal, float* depth);
 void ophys_probe_box_box_sat(const float* cenA, const float* rotA, const float* cenB, const float* rotB,
                              int* overlap, int* axisIdx, float* depth);
 V3 ophys_pad_pos(int pad);

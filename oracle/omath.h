@@ -23,13 +23,13 @@
  * Pinned by the reference's own known-answer tests, its tables, closed forms,
  * linear-programming SAT checks, brute-force mesh searches and physics laws
  * (momentum, restitution, Coulomb friction, spring equilibrium, rolling) on
- * isolated contacts (tests/).
+ * isolated contacts, the game's published control numbers (jump, dodge, flip,
+ * air control, drive and brake, steering radius, autoroll) and brute-force
+ * contact geometry (clip polygons, edge closest points, support corners, the
+ * kept manifold contact) (tests/).
  * PARITY UNPINNED (no independent check; engine and oracle agree with each
- * other only): the ground drive and wheel friction curves, the jump impulse
- * timeline, flip impulses and torques, air-control torques and damping,
- * auto-roll; among several car-mesh clip contacts, which one is kept and its
- * car-side point; the edge-edge contacts of car-mesh and car-car SAT and the
- * car-side internal-edge adjustment.
+ * other only): the car-side seam adjustment for non-coplanar internal edges;
+ * the powerslide steering blend and lateral friction under slip.
  */
 #ifndef CARL_ORACLE_MATH_H
 #define CARL_ORACLE_MATH_H

@@ -763,7 +763,45 @@ static OContact edge_edge_contact(const OTriClip* tc, float minPen, int axisIdx,
     return r;
 }
 
-/* include/Physics/CarArena/Clip.cuh:244-377 */
+/* Contacts of one SAT-overlapping triangle (box-local vertices): the
+ * edge-edge contact for an edge axis, else the triangle clipped to the
+ * witness face's side planes (include/Physics/CarArena/Clip.cuh:244-377). */
+static int clip_pair(const OTriClip* tc, int axisIdx, float minPen, V3 sep, OContact* out)
+{
+    if (axisIdx >= 4) {
+        out[0] = edge_edge_contact(tc, minPen, axisIdx, sep);
+        return 1;
+    }
+    V3 bufA[MAX_PAIR_CONTACTS], bufB[MAX_PAIR_CONTACTS];
+    V3* in = bufA; V3* o = bufB;
+    const int faceAxis = vargmax(vabs(sep));
+    int cnt = 3;
+    in[0] = tc->t.v0; in[1] = tc->t.v1; in[2] = tc->t.v2;
+    for (int a = 0; a < 3 && cnt > 0; a++) {
+        if (a == faceAxis) continue;
+        for (int sg = 1; sg >= -1 && cnt > 0; sg -= 2) {
+            cnt = clip_plane(in, cnt, o, vscale(v_axis(a), (float)sg), vget(K_CAR_HALF, a));
+            V3* sw = in; in = o; o = sw;
+        }
+    }
+    /* writeFaceContacts */
+    const V3 faceNormal = vscale(v_axis(faceAxis), -copysignf(1.f, vget(sep, faceAxis)));
+    const float faceDist = vget(K_CAR_HALF, faceAxis);
+    const float minDepth = -(minPen + K_CONTACT_BREAK);
+    int k = 0;
+    for (int i = 0; i < cnt; i++) {
+        float depth = vdot(faceNormal, in[i]) - faceDist;
+        depth = o_max(depth, minDepth);
+        if (depth > K_CONTACT_BREAK) continue;
+        OContact* ct = &out[k++];
+        ct->carPos = vadd(in[i], vscale(sep, depth));
+        ct->arenaPos = in[i];
+        ct->normal = sep;
+        ct->depth = -depth;
+    }
+    return k;
+}
+
 static void car_arena_clip(OWorld* w, int ci)
 {
     OCar* c = &w->cars[ci];
@@ -772,40 +810,7 @@ static void car_arena_clip(OWorld* w, int ci)
         const OHit* h = &c->hits[p];
         OTriClip tc;
         load_tri_clip(w, h, &tc);
-        if (h->axisIdx >= 4) {
-            c->contacts[p][0] = edge_edge_contact(&tc, h->minPen, h->axisIdx, h->minAxis);
-            c->conCount[p] = 1;
-            continue;
-        }
-        V3 bufA[MAX_PAIR_CONTACTS], bufB[MAX_PAIR_CONTACTS];
-        V3* in = bufA; V3* out = bufB;
-        const V3 sep = h->minAxis;
-        const int faceAxis = vargmax(vabs(sep));
-        int cnt = 3;
-        in[0] = tc.t.v0; in[1] = tc.t.v1; in[2] = tc.t.v2;
-        for (int a = 0; a < 3 && cnt > 0; a++) {
-            if (a == faceAxis) continue;
-            for (int sg = 1; sg >= -1 && cnt > 0; sg -= 2) {
-                cnt = clip_plane(in, cnt, out, vscale(v_axis(a), (float)sg), vget(K_CAR_HALF, a));
-                V3* sw = in; in = out; out = sw;
-            }
-        }
-        /* writeFaceContacts */
-        const V3 faceNormal = vscale(v_axis(faceAxis), -copysignf(1.f, vget(sep, faceAxis)));
-        const float faceDist = vget(K_CAR_HALF, faceAxis);
-        const float minDepth = -(h->minPen + K_CONTACT_BREAK);
-        int k = 0;
-        for (int i = 0; i < cnt; i++) {
-            float depth = vdot(faceNormal, in[i]) - faceDist;
-            depth = o_max(depth, minDepth);
-            if (depth > K_CONTACT_BREAK) continue;
-            OContact* ct = &c->contacts[p][k++];
-            ct->carPos = vadd(in[i], vscale(sep, depth));
-            ct->arenaPos = in[i];
-            ct->normal = sep;
-            ct->depth = -depth;
-        }
-        c->conCount[p] = k;
+        c->conCount[p] = clip_pair(&tc, h->axisIdx, h->minPen, h->minAxis, c->contacts[p]);
     }
 }
 
@@ -2498,6 +2503,70 @@ void ophys_probe_box_tri_sat(const float* tri, int* overlap, int* axisIdx, float
     *axisIdx = s.axisIdx;
     *depth = s.minPen;
     axis[0] = s.minAxis.x; axis[1] = s.minAxis.y; axis[2] = s.minAxis.z;
+}
+
+/* The arena manifold of car ci built from the current state: broadphase,
+ * SAT, clip, then the plane points and the best mesh contact
+ * (include/Physics/CarArena/Manifold.cuh:198-310) */
+int ophys_probe_manifold(OWorld* w, int ci, float* carPos, float* worldPos, float* normal, float* dist)
+{
+    ophys_broadphase(w, ci);
+    car_arena_sat(w, ci);
+    car_arena_clip(w, ci);
+    OManPoint pts[MAX_MANIFOLD];
+    const int n = build_manifold(w, ci, pts);
+    for (int i = 0; i < n; i++) {
+        const float* src[3] = { &pts[i].carPos.x, &pts[i].worldPos.x, &pts[i].worldNormal.x };
+        float* dst[3] = { carPos + 3 * i, worldPos + 3 * i, normal + 3 * i };
+        for (int k = 0; k < 3; k++) { dst[k][0] = src[k][0]; dst[k][1] = src[k][1]; dst[k][2] = src[k][2]; }
+        dist[i] = pts[i].dist;
+    }
+    return n;
+}
+
+/* SAT and clip contacts of one triangle given in box-local coordinates,
+ * as the car-arena stages generate them (no internal-edge adjustment) */
+int ophys_probe_box_tri_contacts(const float* tri, int* axisIdx, float* carPos, float* arenaPos, float* normal,
+                                 float* depth)
+{
+    OTriClip tc;
+    tri_set(&tc.t, v3(tri[0], tri[1], tri[2]), v3(tri[3], tri[4], tri[5]), v3(tri[6], tri[7], tri[8]));
+    tc.t.delta = vneg(tri_center(&tc.t));
+    tc.faceNormal = vnorm(vcross(tc.t.e0, vsub(tc.t.v2, tc.t.v0)));
+    tc.angles = v3(K_BOUNDARY_EDGE_ANGLE, K_BOUNDARY_EDGE_ANGLE, K_BOUNDARY_EDGE_ANGLE);
+    const OSat s = tri_sat(&tc.t);
+    *axisIdx = s.overlap ? s.axisIdx : -1;
+    if (!s.overlap) return 0;
+    OContact ct[MAX_PAIR_CONTACTS];
+    const int n = clip_pair(&tc, s.axisIdx, s.minPen, s.minAxis, ct);
+    for (int i = 0; i < n; i++) {
+        const float* src[3] = { &ct[i].carPos.x, &ct[i].arenaPos.x, &ct[i].normal.x };
+        float* dst[3] = { carPos + 3 * i, arenaPos + 3 * i, normal + 3 * i };
+        for (int k = 0; k < 3; k++) { dst[k][0] = src[k][0]; dst[k][1] = src[k][1]; dst[k][2] = src[k][2]; }
+        depth[i] = ct[i].depth;
+    }
+    return n;
+}
+
+/* SAT and contacts of two car hitboxes given in world coordinates, as the
+ * car-car stage generates them; points in each box's local frame */
+int ophys_probe_box_box_contacts(const float* cenA, const float* rotA, const float* cenB, const float* rotB,
+                                 int* axisIdx, float* carPosA, float* carPosB, float* normal, float* depth)
+{
+    const OBox A = { v3(cenA[0], cenA[1], cenA[2]), q4(rotA[0], rotA[1], rotA[2], rotA[3]) };
+    const OBox B = { v3(cenB[0], cenB[1], cenB[2]), q4(rotB[0], rotB[1], rotB[2], rotB[3]) };
+    const OSat s = cc_sat(&A, &B);
+    *axisIdx = s.overlap ? s.axisIdx : -1;
+    if (!s.overlap) return 0;
+    OCC cts[MAX_MANIFOLD];
+    const int n = cc_contacts(&s, &A, &B, cts);
+    for (int i = 0; i < n; i++) {
+        const float* src[3] = { &cts[i].carPosA.x, &cts[i].carPosB.x, &cts[i].normal.x };
+        float* dst[3] = { carPosA + 3 * i, carPosB + 3 * i, normal + 3 * i };
+        for (int k = 0; k < 3; k++) { dst[k][0] = src[k][0]; dst[k][1] = src[k][1]; dst[k][2] = src[k][2]; }
+        depth[i] = cts[i].depth;
+    }
+    return n;
 }
 
 /* box-box SAT of two car hitboxes (CarCar/SAT.cuh:46-125) */

@@ -58,6 +58,9 @@ def lib():
         L.oracle_probe_steer_stage.argtypes = [C.c_float, fp, fp]
         L.oracle_kickoff_perm.argtypes = [C.c_int, C.c_int]
         L.oracle_probe_box_tri_sat.argtypes = [fp, ip, ip, fp, fp]
+        L.oracle_probe_box_tri_contacts.argtypes = [fp, ip, fp, fp, fp, fp]
+        L.oracle_probe_box_box_contacts.argtypes = [fp, fp, fp, fp, ip, fp, fp, fp, fp]
+        L.oracle_probe_manifold.argtypes = [vp, C.c_int, fp, fp, fp, fp]
         L.oracle_probe_box_box_sat.argtypes = [fp, fp, fp, fp, ip, ip, fp]
         L.oracle_hash32.restype = C.c_uint32
         L.oracle_hash32.argtypes = [C.c_uint32]
