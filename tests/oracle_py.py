@@ -107,7 +107,7 @@ class OracleEnv:
         self.n_cars = n_blue + n_orange
 
     def close(self):
-        if self.h:
+        if getattr(self, "h", None):
             lib().oracle_destroy(self.h)
             self.h = None
 
