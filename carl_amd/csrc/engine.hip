@@ -1448,6 +1448,56 @@ int carl_env_import_state(carl_env* e, const uint32_t* car, const uint32_t* sim,
     return CARL_OK;
 }
 
+int carl_env_pack_rewards_dones(carl_env* e)
+{
+    CARL_TRY(checkEnv(e));
+    return packRewardsDones(e);
+}
+
+int carl_env_pack_transition_state(carl_env* e, int touchWindow)
+{
+    CARL_TRY(checkEnv(e));
+    if (touchWindow < 1) return fail(CARL_ERR_VALUE, "touch window must be at least 1");
+    return packState(e, e->tstate, touchWindow, nullptr);
+}
+
+int carl_env_pack_transition_obs(carl_env* e)
+{
+    CARL_TRY(checkEnv(e));
+    return packObs(e, e->tobs, e->dones);
+}
+
+int carl_env_pack_match_state(carl_env* e, const uint8_t* mask)
+{
+    CARL_TRY(checkEnv(e));
+    return packMatch(e, (const bool*)mask);
+}
+
+int carl_env_pack_obs(carl_env* e, const uint8_t* mask)
+{
+    CARL_TRY(checkEnv(e));
+    return packObs(e, e->obs, (const bool*)mask);
+}
+
+int carl_env_pack_state(carl_env* e, const uint8_t* mask)
+{
+    CARL_TRY(checkEnv(e));
+    return packState(e, e->state, 1, (const bool*)mask);
+}
+
+int carl_env_set_actions(carl_env* e, int kind, const void* actions)
+{
+    CARL_TRY(checkEnv(e));
+    if (!actions) return fail(CARL_ERR_VALUE, "null actions");
+    void* dst = nullptr;
+    if (kind == CARL_ACTIONS_DISCRETE) dst = e->actions;
+    else if (kind == CARL_ACTIONS_CONTINUOUS) dst = e->cactions;
+    else return fail(CARL_ERR_VALUE, "actions kind must be discrete or continuous");
+    HIP_TRY(hipMemcpyAsync(dst, actions, sizeof(uint32_t) * 7 * (size_t)e->nTotal, hipMemcpyDeviceToDevice,
+                           e->stream));
+    return CARL_OK;
+}
+
 int carl_exclusive_scan_i32(const int32_t* in, int32_t* out, int n, void* stream)
 {
     if (n < 0) return fail(CARL_ERR_VALUE, "negative length");

@@ -28,6 +28,14 @@
  *                                                        python/carl.cu:782-818
  *   carl_env_stream        <- RLEnvironment::getStream   include/RLEnvironment.cuh:61
  *   carl_env_synchronize   <- cudaStreamSynchronize calls python/carl.cu:419,505,663
+ *   carl_env_pack_rewards_dones    <- EnvIO::packRewardsDones    src/EnvIO.cu:466-484
+ *   carl_env_pack_transition_state <- EnvIO::packTransitionState src/EnvIO.cu:442-448
+ *   carl_env_pack_transition_obs   <- EnvIO::packTransitionObs   src/EnvIO.cu:458-464
+ *   carl_env_pack_match_state      <- EnvIO::packRawMatchState   src/EnvIO.cu:486-497
+ *   carl_env_pack_obs              <- EnvIO::packObs             src/EnvIO.cu:450-456
+ *   carl_env_pack_state            <- EnvIO::packState           src/EnvIO.cu:434-440
+ *   carl_env_set_actions           <- EnvIO::setActions / setContinuousActions
+ *                                                                src/EnvIO.cu:565-577
  *   carl_exclusive_scan_i32 <- PrefixSum::scanOnStream   src/RLEnvironment.cu:18-38
  *
  * carl_env_enable_timing / carl_env_tick_timing / carl_tick_kernel_name have no
@@ -244,6 +252,25 @@ int carl_env_reset(carl_env* env);
 
 /* Reset simulations whose episode ended (goal, timeouts, overtime expiry). */
 int carl_env_reset_dones(carl_env* env);
+
+/* ---- EnvIO packs (for C++ hosts composing the step themselves) ----------
+ * The step's post-tick sequence of python/carl.cu:359-367 is
+ *   pack_rewards_dones; pack_transition_state(frameskip);
+ *   pack_transition_obs; reset_dones; pack_match_state(NULL); pack_obs(NULL);
+ *   pack_state(NULL)
+ * and carl_env_step runs exactly that (fused) after its ticks.  reset_mask
+ * (bool [n_sim], device) restricts a pack to the selected simulations; NULL
+ * packs every simulation.  All are queued on the environment stream. */
+int carl_env_pack_rewards_dones(carl_env* env);
+int carl_env_pack_transition_state(carl_env* env, int touch_window);
+int carl_env_pack_transition_obs(carl_env* env);   /* rows of the simulations whose done flag is set */
+int carl_env_pack_match_state(carl_env* env, const uint8_t* reset_mask);
+int carl_env_pack_obs(carl_env* env, const uint8_t* reset_mask);
+int carl_env_pack_state(carl_env* env, const uint8_t* reset_mask);
+/* Copy a step's actions (device pointer, CARL_ACTIONS_DISCRETE int32 or
+ * CARL_ACTIONS_CONTINUOUS float [n_sim, n_cars, 7]) into the environment's
+ * action buffer (CARL_BUF_ACTIONS / CARL_BUF_CONTINUOUS_ACTIONS). */
+int carl_env_set_actions(carl_env* env, int kind, const void* actions);
 
 /* ---- state setters --------------------------------------------------------
  * Row r of each input belongs to simulation indices[r] (int64, device) when
