@@ -481,10 +481,30 @@ public:
 
     void resetDones() { check(carl_env_reset_dones(env_)); }
     void synchronize() { check(carl_env_synchronize(env_)); }
-    void enableTiming(bool on, bool ticks, bool packing)
+    void enableTiming(bool on, bool ticks, bool packing, bool stages)
     {
-        const int flags = (ticks ? CARL_TIME_TICKS : 0) | (packing ? CARL_TIME_PACKING : 0);
+        const int flags = (ticks ? CARL_TIME_TICKS : 0) | (packing ? CARL_TIME_PACKING : 0)
+                          | (stages ? CARL_TIME_STAGES : 0);
         check(carl_env_enable_timing(env_, on ? flags : 0));
+    }
+    py::dict stageTiming()
+    {
+        double us[CARL_STAGES], last[CARL_STAGES + 1], spanUs = 0.0, launchUs = 0.0;
+        int ticks = 0;
+        check(carl_env_stage_timing(env_, us, last, &spanUs, &launchUs, &ticks));
+        py::dict stages, critical;
+        for (int s = 0; s < CARL_STAGES; s++) {
+            stages[py::str(carl_stage_name(s))] = us[s];
+            critical[py::str(carl_stage_name(s))] = last[s];
+        }
+        critical["start delay"] = last[CARL_STAGES];
+        py::dict out;
+        out["stages"] = stages;
+        out["last_workgroup"] = critical;
+        out["span_us"] = spanUs;
+        out["launch_us"] = launchUs;
+        out["ticks"] = ticks;
+        return out;
     }
     py::dict tickTiming()
     {
@@ -647,7 +667,8 @@ PYBIND11_MODULE(_carl, m)
         .def("reset_dones", &Env::resetDones)
         .def("synchronize", &Env::synchronize)
         .def("enable_tick_timing", &Env::enableTiming, py::arg("enable") = true, py::arg("ticks") = true,
-             py::arg("packing") = false)
+             py::arg("packing") = false, py::arg("stages") = false)
         .def("tick_timing", &Env::tickTiming)
+        .def("stage_timing", &Env::stageTiming)
         .def_property_readonly("tick_count", [](Env& e) { return e.param(CARL_PARAM_TICK_COUNT); });
 }

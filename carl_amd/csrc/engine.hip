@@ -49,6 +49,12 @@ int fail(int code, const std::string& msg)
             return fail(CARL_ERR_RUNTIME, std::string(#expr) + ": " + hipGetErrorString(e_)); \
     } while (0)
 
+#define CARL_TRY(expr)                 \
+    do {                               \
+        const int rc_ = (expr);        \
+        if (rc_ != CARL_OK) return rc_; \
+    } while (0)
+
 // ------------------------------------------------------------------ kernels
 
 constexpr int kTickBlock = 256;
@@ -304,40 +310,82 @@ constexpr int kDefaultWindowSims = 64;
 #endif
 constexpr int kWindowContactDepth = CARL_WINDOW_CONTACT_DEPTH;
 
-// The waves' contact-search and ball-gather areas share one LDS block, and
-// one wave's ball area overlaps another wave's contact area (ball[1] lies
-// inside contact[0]).  Every phase change of the window kernel is therefore a
-// workgroup barrier: no wave may start a tick's contact search while another
-// is still in the previous tick's ball phase.
-union WindowLds {
+// Each wave's contact-search and ball-gather areas have LDS of their own
+// (35.4 KB per workgroup; four workgroups per CU, the occupancy the 256-VGPR
+// budget allows, use 141 KB of the 160 KB), so no wave can overwrite another
+// wave's area whatever the phase order.  The phases are still separated by
+// workgroup barriers: a phase reads state words other threads of the
+// workgroup wrote in the phase before.
+struct WindowLds {
     ContactLds contact[kWindowWaves];
     BallLds ball[kWindowWaves];
 };
+static_assert(4 * sizeof(WindowLds) <= 160 * 1024, "four window workgroups per CU");
 
-// two waves per SIMD (the second bound is waves per execution unit): 256 VGPRs
-__global__ __launch_bounds__(kWindowBlock, 2) void tickWindowKernel(Dev d, uint32_t* __restrict__ ws, int screen,
-                                                                 int kind, const void* __restrict__ actions,
-                                                                 int tick0, int ticks, int simsPerBlock,
-                                                                 SimRange range)
+// Phases of a tick in the window kernel, timed by the stage profile.
+enum WindowStage { kStageContact, kStageCarArena, kStageBall, kStageFinish, kStagePads, kWindowStages };
+static_assert(kWindowStages == CARL_STAGES && kStagePads == CARL_STAGE_PADS, "stage ids of the C-ABI");
+
+// Stage-profile counters (64-bit wall-clock ticks), summed over launches
+// except the three per-launch words, which the last workgroup of a launch
+// to finish resets (kProfFirst to all ones, the others to zero).
+enum ProfWord {
+    kProfStages = 0,                      // [stage]: all workgroups' time in the stage
+    kProfLast = kProfStages + kWindowStages,  // [stage]: the stages of each launch's last workgroup
+    kProfLastDelay = kProfLast + kWindowStages,  // that workgroup's start after the launch's first start
+    kProfSpan,                            // first workgroup start to last workgroup end
+    kProfFirst,                           // per launch: earliest workgroup start
+    kProfEnd,                             // per launch: latest workgroup end
+    kProfDone,                            // per launch: workgroups finished
+    kProfWords
+};
+
+// The window kernel's body.  With Profile, thread 0 of each workgroup reads
+// the wall clock (the constant-rate counter) at the start and after every
+// phase barrier; a phase's time runs from the barrier before it to its own,
+// barrier wait included.  At the end each workgroup adds its phase times to
+// the kProfStages sums, and the launch's last workgroup to finish adds its
+// own phase times, its start delay and the launch's span.  Without Profile
+// the code is the plain kernel.
+template <bool Profile>
+DI void tickWindowBody(Dev d, uint32_t* __restrict__ ws, int screen, int kind, const void* __restrict__ actions,
+                       int tick0, int ticks, int simsPerBlock, SimRange range, unsigned long long* __restrict__ prof)
 {
     __shared__ WindowLds L;
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
     const int sim0 = range.begin + blockIdx.x * simsPerBlock;
     const int simEnd = min(sim0 + simsPerBlock, range.end);
     const int car0 = sim0 * d.nCars, carEnd = simEnd * d.nCars;
+    unsigned long long acc[kWindowStages] = {}, first = 0, last = 0;
+    auto mark = [&](int stage) {
+        if constexpr (Profile) {
+            if (t == 0) {
+                const unsigned long long now = wall_clock64();
+                acc[stage] += now - last;
+                last = now;
+            }
+        }
+    };
+    if constexpr (Profile) {
+        if (t == 0) first = last = wall_clock64();
+    }
     for (int k = 0; k < ticks; k++) {
         const int tick = tick0 + k;
         for (int g = car0 + wave * kContactOwners; g < carEnd; g += kWindowWaves * kContactOwners)
             contactGroup<kWindowContactDepth>(d, ws, screen, g, carEnd, L.contact[wave], lane);
         __syncthreads();
+        mark(kStageContact);
         for (int c = car0 + t; c < carEnd; c += kWindowBlock) carArenaCar(d, ws, kind, actions, tick, c);
         __syncthreads();
+        mark(kStageCarArena);
         for (int g = sim0 + wave * kBallOwners; g < simEnd; g += kWindowWaves * kBallOwners)
             ballGroup(d, tick, g, simEnd, L.ball[wave], lane);
         __syncthreads();
+        mark(kStageBall);
         for (int c = car0 + t; c < carEnd; c += kWindowBlock) finishCar(d, c);
         for (int s = sim0 + t; s < simEnd; s += kWindowBlock) finishBall(d, s);
         __syncthreads();
+        mark(kStageFinish);
         {
             // boost pads: the workgroup's threads split into kWindowBlock /
             // simsPerBlock parts, each taking a contiguous range of every
@@ -352,7 +400,47 @@ __global__ __launch_bounds__(kWindowBlock, 2) void tickWindowKernel(Dev d, uint3
                 boostPadsRange(d, sim0 + j, kPads * q / parts, kPads * (q + 1) / parts);
         }
         __syncthreads();
+        mark(kStagePads);
     }
+    if constexpr (Profile) {
+        if (t == 0) {
+            for (int st = 0; st < kWindowStages; st++) atomicAdd(&prof[kProfStages + st], acc[st]);
+            atomicMin(&prof[kProfFirst], first);
+            atomicMax(&prof[kProfEnd], last);
+            __threadfence();
+            if (atomicAdd(&prof[kProfDone], 1ull) == gridDim.x - 1) {
+                // every other workgroup has published its start and end
+                __threadfence();
+                const unsigned long long first0 = atomicMin(&prof[kProfFirst], ~0ull);
+                const unsigned long long end1 = atomicMax(&prof[kProfEnd], 0ull);
+                for (int st = 0; st < kWindowStages; st++) atomicAdd(&prof[kProfLast + st], acc[st]);
+                atomicAdd(&prof[kProfLastDelay], first - first0);
+                atomicAdd(&prof[kProfSpan], end1 - first0);
+                atomicExch(&prof[kProfFirst], ~0ull);
+                atomicExch(&prof[kProfEnd], 0ull);
+                atomicExch(&prof[kProfDone], 0ull);
+            }
+        }
+    }
+}
+
+// two waves per SIMD (the second bound is waves per execution unit): 256 VGPRs
+__global__ __launch_bounds__(kWindowBlock, 2) void tickWindowKernel(Dev d, uint32_t* __restrict__ ws, int screen,
+                                                                 int kind, const void* __restrict__ actions,
+                                                                 int tick0, int ticks, int simsPerBlock,
+                                                                 SimRange range)
+{
+    tickWindowBody<false>(d, ws, screen, kind, actions, tick0, ticks, simsPerBlock, range, nullptr);
+}
+
+// the same kernel with the stage profile
+__global__ __launch_bounds__(kWindowBlock, 2) void tickWindowProfileKernel(Dev d, uint32_t* __restrict__ ws,
+                                                                        int screen, int kind,
+                                                                        const void* __restrict__ actions, int tick0,
+                                                                        int ticks, int simsPerBlock, SimRange range,
+                                                                        unsigned long long* __restrict__ prof)
+{
+    tickWindowBody<true>(d, ws, screen, kind, actions, tick0, ticks, simsPerBlock, range, prof);
 }
 
 __global__ void resetKernel(Dev d, int nOrange)
@@ -796,11 +884,25 @@ struct carl_env {
     hipEvent_t fork = nullptr, join[kMaxTickStreams - 1] = {};
     int windowSims = kDefaultWindowSims;  // simulations per block of the tick-window kernel (0: phase kernels)
     int timing = 0;                      // CARL_TIME_* flags
-    // timing: per timed launch a start and an end event (reusable pool) and
-    // the launch's kernel id
+    // timing: a start and an end event per timed launch not yet folded
+    // (a pool of at most kTimedPool pairs) and the launch's kernel id;
+    // folding adds their durations to the sums below
     size_t timedLaunches = 0;
     std::vector<hipEvent_t> marks;
     std::vector<int> markKernel;
+    double kernelMs[CARL_TICK_KERNELS] = {};
+    int kernelLaunches[CARL_TICK_KERNELS] = {};
+    // stage profile (CARL_TIME_STAGES): the window kernel's clock counters
+    // (kProfWords), the launch durations of the profiled ticks, their count,
+    // and the workgroups one profiled launch keeps resident together
+    unsigned long long* prof = nullptr;
+    double stageKernelMs[CARL_TICK_KERNELS] = {};
+    int stageTicks = 0;
+    int stagePath = 0;  // 1: window kernel, 2: phase kernels
+    int profResident = 0;  // window workgroups the device holds at once
+    int profSlots = 0;     // of those, the ones a profiled launch fills
+    bool profMixed = false;  // profiled launches of different shapes
+    double clockMHz = 0.0;  // the wall clock read by wall_clock64
 
     Dev dev() const
     {
@@ -828,7 +930,7 @@ void freeAll(carl_env* e)
     void* ptrs[] = { e->car, e->sim, e->rec, e->cellStart, e->angles, e->triRec, e->refBox, e->refAng, e->fineRec,
                      e->fineAux, e->fineStart, e->obs, e->tobs, e->state, e->tstate, e->rewards, e->dones,
                      e->overtime, e->tovertime, e->score, e->ticks, e->tscore, e->tticks, e->actions, e->cactions,
-                     e->ws };
+                     e->ws, e->prof };
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
     for (hipEvent_t ev : e->marks) (void)hipEventDestroy(ev);
@@ -840,12 +942,45 @@ void freeAll(carl_env* e)
     if (e->stream) (void)hipStreamDestroy(e->stream);
 }
 
+constexpr size_t kTimedPool = 1024;  // event pairs held before folding
+
+// Zeroes the stage-profile counters, the per-launch earliest start to all ones.
+int clearProfile(carl_env* e)
+{
+    unsigned long long init[kProfWords] = {};
+    init[kProfFirst] = ~0ull;
+    HIP_TRY(hipMemcpy(e->prof, init, sizeof init, hipMemcpyHostToDevice));
+    return CARL_OK;
+}
+
+// Adds the durations of the recorded launches to the per-kernel sums (and,
+// with the stage profile on, to its launch sums) and frees their events for
+// reuse.  Timed launches are on the environment stream.
+int foldTiming(carl_env* e)
+{
+    if (e->timedLaunches == 0) return CARL_OK;
+    HIP_TRY(hipStreamSynchronize(e->stream));
+    for (size_t i = 0; i < e->timedLaunches; i++) {
+        float ms = 0.f;
+        HIP_TRY(hipEventElapsedTime(&ms, e->marks[2 * i], e->marks[2 * i + 1]));
+        const int k = e->markKernel[i];
+        e->kernelMs[k] += ms;
+        e->kernelLaunches[k]++;
+        if ((e->timing & CARL_TIME_STAGES) && k != CARL_KERNEL_STEP_ENV) e->stageKernelMs[k] += ms;
+    }
+    e->timedLaunches = 0;
+    return CARL_OK;
+}
+
 // Timing events of the next timed launch: a start and an end event from a
-// reusable pool (created on first use), both null when timing is off.
+// pool (created on first use; when all kTimedPool pairs hold unread
+// launches, those are folded first), both null when timing is off.
 int timedPair(carl_env* e, int kernel, hipEvent_t* begin, hipEvent_t* end)
 {
     *begin = *end = nullptr;
-    if (!(e->timing & (kernel == CARL_KERNEL_STEP_ENV ? CARL_TIME_PACKING : CARL_TIME_TICKS))) return CARL_OK;
+    const int want = kernel == CARL_KERNEL_STEP_ENV ? CARL_TIME_PACKING : (CARL_TIME_TICKS | CARL_TIME_STAGES);
+    if (!(e->timing & want)) return CARL_OK;
+    if (e->timedLaunches == kTimedPool) CARL_TRY(foldTiming(e));
     const size_t slot = 2 * e->timedLaunches;
     while (e->marks.size() < slot + 2) {
         hipEvent_t ev;
@@ -907,9 +1042,20 @@ int launchTicks(carl_env* e, int kind, const void* actions, int n)
         for (int p = 0; p < parts; p++) {
             const SimRange r = range[p];
             const bool timed = p == 0;
-            CARL_MARK(launchTick(e, timed, CARL_KERNEL_WINDOW, tickWindowKernel, dim3(e->grid(r.end - r.begin, wsb)),
-                                 dim3(kWindowBlock), 0, stream[p], d, e->ws, e->contactScreen, kind, actions,
-                                 e->tickCount + 1, n, wsb, r));
+            const int blocks = e->grid(r.end - r.begin, wsb);
+            if (timed && (e->timing & CARL_TIME_STAGES)) {
+                // the clock sums are divided by one resident-workgroup count
+                const int slots = std::min(blocks, e->profResident);
+                if (e->profSlots != 0 && e->profSlots != slots) e->profMixed = true;
+                e->profSlots = slots;
+                CARL_MARK(launchTick(e, timed, CARL_KERNEL_WINDOW, tickWindowProfileKernel, dim3(blocks),
+                                     dim3(kWindowBlock), 0, stream[p], d, e->ws, e->contactScreen, kind, actions,
+                                     e->tickCount + 1, n, wsb, r, e->prof));
+            } else {
+                CARL_MARK(launchTick(e, timed, CARL_KERNEL_WINDOW, tickWindowKernel, dim3(blocks), dim3(kWindowBlock),
+                                     0, stream[p], d, e->ws, e->contactScreen, kind, actions, e->tickCount + 1, n,
+                                     wsb, r));
+            }
         }
     }
     for (int k = 0; e->windowSims == 0 && k < n; k++) {
@@ -933,6 +1079,12 @@ int launchTicks(carl_env* e, int kind, const void* actions, int n)
     for (int p = 1; p < parts; p++) {
         HIP_TRY(hipEventRecord(e->join[p - 1], stream[p]));
         HIP_TRY(hipStreamWaitEvent(e->stream, e->join[p - 1], 0));
+    }
+    if (e->timing & CARL_TIME_STAGES) {
+        const int path = e->windowSims > 0 ? 1 : 2;
+        if (e->stagePath != 0 && e->stagePath != path) e->profMixed = true;
+        e->stagePath = path;
+        e->stageTicks += n;
     }
     e->tickCount += n;
     return CARL_OK;
@@ -968,12 +1120,6 @@ int packRewardsDones(carl_env* e)
     HIP_TRY(hipGetLastError());
     return CARL_OK;
 }
-
-#define CARL_TRY(expr)                 \
-    do {                               \
-        const int rc_ = (expr);        \
-        if (rc_ != CARL_OK) return rc_; \
-    } while (0)
 
 int initialPacks(carl_env* e)
 {
@@ -1380,8 +1526,26 @@ int carl_env_enable_timing(carl_env* e, int enable)
 {
     CARL_TRY(checkEnv(e));
     HIP_TRY(hipStreamSynchronize(e->stream));
-    e->timing = enable & (CARL_TIME_TICKS | CARL_TIME_PACKING);
+    e->timing = enable & (CARL_TIME_TICKS | CARL_TIME_PACKING | CARL_TIME_STAGES);
     e->timedLaunches = 0;
+    for (int k = 0; k < CARL_TICK_KERNELS; k++) {
+        e->kernelMs[k] = e->stageKernelMs[k] = 0.0;
+        e->kernelLaunches[k] = 0;
+    }
+    e->stageTicks = e->stagePath = e->profSlots = 0;
+    e->profMixed = false;
+    if (e->timing & CARL_TIME_STAGES) {
+        if (!e->prof) CARL_TRY(devAlloc(&e->prof, kProfWords));
+        CARL_TRY(clearProfile(e));
+        int device = 0, cus = 0, perCu = 0, khz = 0;
+        HIP_TRY(hipGetDevice(&device));
+        HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
+        HIP_TRY(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, device));
+        HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(&perCu, tickWindowProfileKernel, kWindowBlock, 0));
+        if (khz <= 0 || perCu <= 0) return fail(CARL_ERR_RUNTIME, "no wall-clock rate or window occupancy");
+        e->profResident = perCu * cus;
+        e->clockMHz = khz / 1000.0;
+    }
     return CARL_OK;
 }
 
@@ -1389,19 +1553,68 @@ int carl_env_tick_timing(carl_env* e, double* kernelMs, int* launches)
 {
     CARL_TRY(checkEnv(e));
     if (!kernelMs || !launches) return fail(CARL_ERR_VALUE, "null output pointer");
+    CARL_TRY(foldTiming(e));
     HIP_TRY(hipStreamSynchronize(e->stream));
     for (int k = 0; k < CARL_TICK_KERNELS; k++) {
-        kernelMs[k] = 0.0;
-        launches[k] = 0;
+        kernelMs[k] = e->kernelMs[k];
+        launches[k] = e->kernelLaunches[k];
+        e->kernelMs[k] = 0.0;
+        e->kernelLaunches[k] = 0;
     }
-    for (size_t i = 0; i < e->timedLaunches; i++) {
-        float ms = 0.f;
-        HIP_TRY(hipEventElapsedTime(&ms, e->marks[2 * i], e->marks[2 * i + 1]));
-        kernelMs[e->markKernel[i]] += ms;
-        launches[e->markKernel[i]]++;
-    }
-    e->timedLaunches = 0;
     return CARL_OK;
+}
+
+int carl_env_stage_timing(carl_env* e, double* stageUs, double* lastUs, double* spanUs, double* launchUs, int* ticks)
+{
+    CARL_TRY(checkEnv(e));
+    if (!stageUs || !lastUs || !spanUs || !launchUs || !ticks) return fail(CARL_ERR_VALUE, "null output pointer");
+    if (!(e->timing & CARL_TIME_STAGES)) return fail(CARL_ERR_VALUE, "the stage profile is not enabled");
+    CARL_TRY(foldTiming(e));
+    HIP_TRY(hipStreamSynchronize(e->stream));
+    const bool mixed = e->profMixed;
+    const int n = e->stageTicks, path = e->stagePath, slots = e->profSlots;
+    unsigned long long clocks[kProfWords] = {};
+    HIP_TRY(hipMemcpy(clocks, e->prof, sizeof clocks, hipMemcpyDeviceToHost));
+    double kernelMs[CARL_TICK_KERNELS];
+    std::copy(e->stageKernelMs, e->stageKernelMs + CARL_TICK_KERNELS, kernelMs);
+    // start the next period
+    CARL_TRY(clearProfile(e));
+    std::fill(e->stageKernelMs, e->stageKernelMs + CARL_TICK_KERNELS, 0.0);
+    e->stageTicks = e->stagePath = e->profSlots = 0;
+    e->profMixed = false;
+    if (mixed) return fail(CARL_ERR_VALUE, "the tick launch shape changed during the stage profile");
+    *ticks = n;
+    *launchUs = *spanUs = 0.0;
+    std::fill(stageUs, stageUs + CARL_STAGES, 0.0);
+    std::fill(lastUs, lastUs + CARL_STAGES + 1, 0.0);
+    if (n == 0) return CARL_OK;
+    if (path == 1) {
+        const double us = 1.0 / (e->clockMHz * n);  // clock ticks -> us per tick
+        // workgroup time of each phase over the workgroups resident at once
+        for (int s = 0; s < CARL_STAGES; s++) {
+            stageUs[s] = clocks[kProfStages + s] * us / slots;
+            lastUs[s] = clocks[kProfLast + s] * us;
+        }
+        lastUs[CARL_STAGES] = clocks[kProfLastDelay] * us;
+        *spanUs = clocks[kProfSpan] * us;
+        *launchUs = kernelMs[CARL_KERNEL_WINDOW] * 1e3 / n;
+    } else {
+        // one phase kernel per stage; the boost pads run in the finish kernel
+        const int kernel[CARL_STAGES - 1] = { CARL_KERNEL_CONTACT, CARL_KERNEL_CAR_ARENA, CARL_KERNEL_BALL,
+                                              CARL_KERNEL_FINISH };
+        for (int s = 0; s < CARL_STAGES - 1; s++) {
+            stageUs[s] = lastUs[s] = kernelMs[kernel[s]] * 1e3 / n;
+            *launchUs += stageUs[s];
+        }
+        *spanUs = *launchUs;
+    }
+    return CARL_OK;
+}
+
+const char* carl_stage_name(int stage)
+{
+    static const char* names[CARL_STAGES] = { "contact", "car-arena", "ball", "finish", "boost-pads" };
+    return stage >= 0 && stage < CARL_STAGES ? names[stage] : "";
 }
 
 const char* carl_tick_kernel_name(int kernel)

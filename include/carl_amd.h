@@ -335,11 +335,13 @@ enum {
 };
 
 /* Timing selection for carl_env_enable_timing (bit flags; 0 turns it off). */
-enum { CARL_TIME_TICKS = 1, CARL_TIME_PACKING = 2 };
+enum { CARL_TIME_TICKS = 1, CARL_TIME_PACKING = 2, CARL_TIME_STAGES = 4 };
 
 /* With timing enabled, HIP events recorded by the dispatch bracket every
- * tick kernel of partition 0 (CARL_TIME_TICKS) and every packing kernel of
- * carl_env_step (CARL_TIME_PACKING).
+ * tick kernel of partition 0 (CARL_TIME_TICKS or CARL_TIME_STAGES) and every
+ * packing kernel of carl_env_step (CARL_TIME_PACKING).  At most 1024 launches'
+ * events are held; the 1025th launch first synchronises the environment
+ * stream and adds their durations to the sums.
  * carl_env_tick_timing synchronises the environment stream and
  * returns, per kernel (arrays of CARL_TICK_KERNELS), the summed duration in
  * ms and the launch count since timing was enabled or last read, then clears
@@ -347,6 +349,50 @@ enum { CARL_TIME_TICKS = 1, CARL_TIME_PACKING = 2 };
 int carl_env_enable_timing(carl_env* env, int enable);
 int carl_env_tick_timing(carl_env* env, double* kernel_ms, int* launches);
 const char* carl_tick_kernel_name(int kernel);
+
+/* ---- stage profile (the reference's PROFILE stages,
+ * include/Cuda/Profiler.cuh:119-162, src/RLEnvironment.cu:166-211) ----------
+ * The phases of a tick.  The reference's nine stages fall into them as:
+ * contact = broad+susp, narrow; car-arena = controls, manifold+solve;
+ * ball = car-car+ball; finish = integrate-cars, impulse-cache;
+ * boost-pads = boost-pads. */
+enum {
+    CARL_STAGE_CONTACT = 0,
+    CARL_STAGE_CAR_ARENA = 1,
+    CARL_STAGE_BALL = 2,
+    CARL_STAGE_FINISH = 3,
+    CARL_STAGE_PADS = 4,
+    CARL_STAGES = 5
+};
+
+/* With CARL_TIME_STAGES enabled, the tick window launches of partition 0 run
+ * a twin of the window kernel in which each workgroup reads the device's
+ * constant-rate wall clock at its start and at every phase barrier (the plain
+ * kernel is left as it is: it is the one measured otherwise).
+ * carl_env_stage_timing synchronises and returns, for the ticks since the
+ * profile was enabled or last read, in us per tick:
+ *   stage_us[CARL_STAGES]  each stage's share of the device: the stage's time
+ *       summed over all workgroups / the workgroups resident at once
+ *       (min(grid, occupancy x CUs)).  Workgroups that finish early leave
+ *       their slots idle until the launch ends, so these sum to less than
+ *       the launch time by the launch's imbalance.
+ *   last_us[CARL_STAGES + 1]  the critical path: the stages of the workgroup
+ *       that finished each launch last, then its start after the launch's
+ *       first workgroup start; they sum to span_us.
+ *   span_us    the launch's first workgroup start to its last workgroup end
+ *       (wall clock).
+ *   launch_us  the launch itself (HIP events).
+ *   ticks      ticks covered;
+ * then clears them.  With the phase kernels each stage is one kernel's
+ * HIP-event time (the boost pads run in the finish kernel: CARL_STAGE_PADS
+ * is 0), in stage_us and last_us alike, and span_us = launch_us = their sum.
+ * It fails with CARL_ERR_VALUE when the profile is off or the tick launch
+ * shape (window size, streams, window/phase path) changed within the period.
+ * With several tick streams only partition 0 is profiled and the figures are
+ * its own; the other partitions share the device. */
+int carl_env_stage_timing(carl_env* env, double* stage_us, double* last_us, double* span_us,
+                          double* launch_us, int* ticks);
+const char* carl_stage_name(int stage);
 
 /* ---- primitives ------------------------------------------------------------ */
 
