@@ -245,6 +245,9 @@ def main() -> None:
                     help="print a markdown summary of rocprofv3 output directories of one bench run "
                          "(use - for an absent one; --steps/--warmup name its window, --copy-mib the copy size)")
     ap.add_argument("--copy-mib", type=int, default=512)
+    ap.add_argument("--stage-profile", action="store_true",
+                    help="after the timed region, run further steps with the stage profile, print its table "
+                         "on stderr and add it to the JSON line")
     args = ap.parse_args()
 
     if args.summarize_rocprof:
@@ -272,6 +275,7 @@ def main() -> None:
 
     import carl_amd
     from carl_amd import workloads
+    from carl_amd.profiler import stage_profile
 
     dev = torch.device("cuda:0")
     n_sim, n_cars = args.n_sim, args.blue + args.orange
@@ -314,6 +318,14 @@ def main() -> None:
         reward = env_step(i)
     timing.update(env.tick_timing())
     env.enable_tick_timing(False)
+    stages = None
+    if args.stage_profile:
+        env.enable_tick_timing(True, ticks=False, stages=True)
+        for i in range(args.steps, args.steps + min(args.steps, 200)):
+            reward = env_step(i)
+        table, stages = stage_profile(env, n_sim // min(env.tick_streams, n_sim))
+        env.enable_tick_timing(False)
+        print(table, file=sys.stderr, flush=True)
     del reward
 
     sim_ticks = n_sim * args.tick_skip * args.steps
@@ -400,6 +412,8 @@ def main() -> None:
                                         args.steps, args.warmup, tag="traffic-after")
             if args.steps <= 200 else None,
         }
+    if stages is not None:
+        result["stage_profile"] = stages
     if args.cpu_ticks > 0:
         result["cpu_baseline"] = cpu_baseline(args.cpu_ticks, args.seed)
     print(json.dumps(result), flush=True)
