@@ -323,4 +323,41 @@ std::string buildArena(const std::string& objPath, HostArena& out)
     return "";
 }
 
+// The reference reads the count, then per triangle mesh, order, three edge
+// angles, flags and three native vertices, all whitespace separated with
+// stream extraction, and checks the stream only once, after the last
+// triangle (src/ArenaMesh.cu:69-99).  A file that cannot be opened reads as a
+// count of 0, so it fails the count check too.
+std::string readArenaMetadata(const char* path, HostArena& out)
+{
+    const int nTris = (int)(out.tris.size() / 3);
+    std::ifstream file(path);
+    int count = 0;
+    file >> count;
+    if (count != nTris) return "CARL arena metadata triangle count mismatch";
+    out.nativeRecords.assign(16 * (size_t)nTris, 0.f);
+    for (int t = 0; t < nTris; t++) {
+        int mesh = 0, order = 0, flags = 0;
+        float a[3] = {}, v[9] = {};
+        file >> mesh >> order >> a[0] >> a[1] >> a[2] >> flags;
+        for (float& x : v) file >> x;
+        // the reference's order key, mesh * 10000 + order, in 32-bit
+        // arithmetic
+        const int32_t key = (int32_t)((uint32_t)mesh * 10000u + (uint32_t)order);
+        float* r = &out.nativeRecords[16 * (size_t)t];
+        const int32_t ints[3] = { key, mesh, flags };
+        for (int k = 0; k < 3; k++) {
+            r[4 * k] = v[3 * k];
+            r[4 * k + 1] = v[3 * k + 1];
+            r[4 * k + 2] = v[3 * k + 2];
+            std::memcpy(&r[4 * k + 3], &ints[k], sizeof(int32_t));
+        }
+        r[12] = a[0];
+        r[13] = a[1];
+        r[14] = a[2];
+    }
+    if (!file) return "Invalid CARL arena metadata";
+    return "";
+}
+
 }  // namespace carl

@@ -21,10 +21,20 @@ struct HostArena {
     std::vector<int> fineStart;     // kFineCells + 1 offsets into fineRecords (in references)
     std::vector<float> fineRecords; // 16 floats per ball-grid reference (record layout), ascending per cell
     std::vector<float> fineAux;     // 4 per ball-grid reference: edge angles xyz, registration range (bits)
+    // native mesh metadata (only with CARL_ARENA_METADATA), 16 floats per
+    // triangle: native vertex 0 xyz, order key (int bits, mesh * 10000 +
+    // order); vertex 1 xyz, native mesh (int bits); vertex 2 xyz, edge flags
+    // (int bits); native edge angles xyz, 0.  Vertices in Bullet units.
+    std::vector<float> nativeRecords;
 };
 
 // Parse, weld and index the mesh.  Returns "" on success, else the error text.
 std::string buildArena(const std::string& objPath, HostArena& out);
+
+// Read the native mesh metadata file (the format tools/arena_metadata.py
+// writes) into out.nativeRecords.  Returns "" on success, else the reference's
+// error text.
+std::string readArenaMetadata(const char* path, HostArena& out);
 
 // Locate arena.obj: $CARL_ARENA_OBJ, then assets/arena.obj next to the package.
 std::string findArenaObj(const std::string& libraryDir);

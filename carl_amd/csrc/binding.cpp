@@ -670,5 +670,6 @@ PYBIND11_MODULE(_carl, m)
              py::arg("packing") = false, py::arg("stages") = false)
         .def("tick_timing", &Env::tickTiming)
         .def("stage_timing", &Env::stageTiming)
-        .def_property_readonly("tick_count", [](Env& e) { return e.param(CARL_PARAM_TICK_COUNT); });
+        .def_property_readonly("tick_count", [](Env& e) { return e.param(CARL_PARAM_TICK_COUNT); })
+        .def_property_readonly("native_arena", [](Env& e) { return e.param(CARL_PARAM_NATIVE_ARENA) != 0; });
 }

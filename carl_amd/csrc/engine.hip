@@ -221,11 +221,20 @@ constexpr int kBallOwners = 32;
 
 // Simulations [sim0, sim0 + kBallOwners) (those below simEnd) by one wave; L
 // is that wave's own LDS.  Every lane of the wave calls it; it synchronises
-// the wave only.
+// the wave only.  With Native (arena metadata) each owner lane gathers and
+// solves its ball against the native meshes alone.
+template <bool Native>
 DI void ballGroup(const Dev& d, int tick, int sim0, int simEnd, BallLds& L, int lane)
 {
     const int sim = sim0 + lane;
     const bool ok = lane < kBallOwners && sim < simEnd;
+    if constexpr (Native) {
+        if (ok) {
+            carCarSim(d, sim, tick);
+            nativeBallTick(d, sim, tick);
+        }
+        return;
+    }
     if (ok) carCarSim(d, sim, tick);
     const bool awake = ok && !ballSleeping(d, sim);
     const V3 center = ok ? d.sv(CARL_SIM_BALL_POS, sim) : kZero;
@@ -273,7 +282,14 @@ DI void ballGroup(const Dev& d, int tick, int sim0, int simEnd, BallLds& L, int 
 __global__ __launch_bounds__(kBallBlock) void ballKernel(Dev d, int tick, SimRange range)
 {
     __shared__ BallLds L;
-    ballGroup(d, tick, range.begin + blockIdx.x * kBallOwners, range.end, L, threadIdx.x);
+    ballGroup<false>(d, tick, range.begin + blockIdx.x * kBallOwners, range.end, L, threadIdx.x);
+}
+
+// the same with the native arena meshes
+__global__ __launch_bounds__(kBallBlock) void ballNativeKernel(Dev d, int tick, SimRange range)
+{
+    __shared__ BallLds L;
+    ballGroup<true>(d, tick, range.begin + blockIdx.x * kBallOwners, range.end, L, threadIdx.x);
 }
 
 // C + D: integration and impulse caches of every car and ball, then the
@@ -299,11 +315,18 @@ __global__ __launch_bounds__(kTickBlock) void finishKernel(Dev d, int simsPerBlo
 // share nothing but the read-only arena, so no other block is ever waited
 // for: a slow wave holds up its own block, not a grid-wide kernel boundary.
 // Two-wave blocks (four per CU) wait less at the phase barriers than
-// four-wave blocks at the same occupancy (measured +1.7% per step); one-wave
-// blocks were 24% slower.
-constexpr int kWindowBlock = 128;
+// four-wave blocks at the same occupancy (measured +1.7% per step), and
+// measured 1-3% faster than one-wave blocks of 32 simulations, whose
+// barriers cost nothing.
+#ifndef CARL_WINDOW_BLOCK
+#define CARL_WINDOW_BLOCK 128
+#endif
+#ifndef CARL_WINDOW_SIMS
+#define CARL_WINDOW_SIMS 64
+#endif
+constexpr int kWindowBlock = CARL_WINDOW_BLOCK;
 constexpr int kWindowWaves = kWindowBlock / 64;
-constexpr int kDefaultWindowSims = 64;
+constexpr int kDefaultWindowSims = CARL_WINDOW_SIMS;
 // rounds of candidate loads the window kernel's contact search keeps in flight
 #ifndef CARL_WINDOW_CONTACT_DEPTH
 #define CARL_WINDOW_CONTACT_DEPTH 1
@@ -347,7 +370,7 @@ enum ProfWord {
 // the kProfStages sums, and the launch's last workgroup to finish adds its
 // own phase times, its start delay and the launch's span.  Without Profile
 // the code is the plain kernel.
-template <bool Profile>
+template <bool Profile, bool Native>
 DI void tickWindowBody(Dev d, uint32_t* __restrict__ ws, int screen, int kind, const void* __restrict__ actions,
                        int tick0, int ticks, int simsPerBlock, SimRange range, unsigned long long* __restrict__ prof)
 {
@@ -379,7 +402,7 @@ DI void tickWindowBody(Dev d, uint32_t* __restrict__ ws, int screen, int kind, c
         __syncthreads();
         mark(kStageCarArena);
         for (int g = sim0 + wave * kBallOwners; g < simEnd; g += kWindowWaves * kBallOwners)
-            ballGroup(d, tick, g, simEnd, L.ball[wave], lane);
+            ballGroup<Native>(d, tick, g, simEnd, L.ball[wave], lane);
         __syncthreads();
         mark(kStageBall);
         for (int c = car0 + t; c < carEnd; c += kWindowBlock) finishCar(d, c);
@@ -430,7 +453,16 @@ __global__ __launch_bounds__(kWindowBlock, 2) void tickWindowKernel(Dev d, uint3
                                                                  int tick0, int ticks, int simsPerBlock,
                                                                  SimRange range)
 {
-    tickWindowBody<false>(d, ws, screen, kind, actions, tick0, ticks, simsPerBlock, range, nullptr);
+    tickWindowBody<false, false>(d, ws, screen, kind, actions, tick0, ticks, simsPerBlock, range, nullptr);
+}
+
+// the same with the native arena meshes
+__global__ __launch_bounds__(kWindowBlock, 2) void tickWindowNativeKernel(Dev d, uint32_t* __restrict__ ws,
+                                                                       int screen, int kind,
+                                                                       const void* __restrict__ actions, int tick0,
+                                                                       int ticks, int simsPerBlock, SimRange range)
+{
+    tickWindowBody<false, true>(d, ws, screen, kind, actions, tick0, ticks, simsPerBlock, range, nullptr);
 }
 
 // the same kernel with the stage profile
@@ -440,7 +472,7 @@ __global__ __launch_bounds__(kWindowBlock, 2) void tickWindowProfileKernel(Dev d
                                                                         int ticks, int simsPerBlock, SimRange range,
                                                                         unsigned long long* __restrict__ prof)
 {
-    tickWindowBody<true>(d, ws, screen, kind, actions, tick0, ticks, simsPerBlock, range, prof);
+    tickWindowBody<true, false>(d, ws, screen, kind, actions, tick0, ticks, simsPerBlock, range, prof);
 }
 
 __global__ void resetKernel(Dev d, int nOrange)
@@ -878,6 +910,8 @@ struct carl_env {
     int32_t* actions = nullptr;
     float* cactions = nullptr;
     uint32_t* ws = nullptr;  // per-tick car workspace (kWsPlanes planes)
+    float4* nativeRec = nullptr;     // native mesh metadata (CARL_ARENA_METADATA), else null
+    float* ballScratch = nullptr;    // with it: kNativeMaxContacts slots of kNativeSlotWords per simulation
     int tickStreams = 1;                 // partitions of the tick, one stream each
     int contactScreen = 1;               // screen (car, triangle) pairs in the contact search
     hipStream_t aux[kMaxTickStreams - 1] = {};
@@ -908,7 +942,8 @@ struct carl_env {
     {
         Dev d;
         d.car = car; d.sim = sim; d.nSim = nSim; d.nBlue = nBlue; d.nCars = nCars; d.nTotal = nTotal; d.seed = seed;
-        d.arena = ArenaView{ rec, cellStart, angles, triRec, refBox, refAng, fineRec, fineAux, fineStart };
+        d.arena = ArenaView{ rec, cellStart, angles, triRec, refBox, refAng, fineRec, fineAux, fineStart, nativeRec };
+        d.ballScratch = ballScratch;
         return d;
     }
     DoneRule rule() const { return DoneRule{ maxTicks, overtimeTicks, noTouchTicks }; }
@@ -930,7 +965,7 @@ void freeAll(carl_env* e)
     void* ptrs[] = { e->car, e->sim, e->rec, e->cellStart, e->angles, e->triRec, e->refBox, e->refAng, e->fineRec,
                      e->fineAux, e->fineStart, e->obs, e->tobs, e->state, e->tstate, e->rewards, e->dones,
                      e->overtime, e->tovertime, e->score, e->ticks, e->tscore, e->tticks, e->actions, e->cactions,
-                     e->ws, e->prof };
+                     e->ws, e->prof, e->nativeRec, e->ballScratch };
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
     for (hipEvent_t ev : e->marks) (void)hipEventDestroy(ev);
@@ -1052,9 +1087,10 @@ int launchTicks(carl_env* e, int kind, const void* actions, int n)
                                      dim3(kWindowBlock), 0, stream[p], d, e->ws, e->contactScreen, kind, actions,
                                      e->tickCount + 1, n, wsb, r, e->prof));
             } else {
-                CARL_MARK(launchTick(e, timed, CARL_KERNEL_WINDOW, tickWindowKernel, dim3(blocks), dim3(kWindowBlock),
-                                     0, stream[p], d, e->ws, e->contactScreen, kind, actions, e->tickCount + 1, n,
-                                     wsb, r));
+                CARL_MARK(launchTick(e, timed, CARL_KERNEL_WINDOW,
+                                     e->nativeRec ? tickWindowNativeKernel : tickWindowKernel, dim3(blocks),
+                                     dim3(kWindowBlock), 0, stream[p], d, e->ws, e->contactScreen, kind, actions,
+                                     e->tickCount + 1, n, wsb, r));
             }
         }
     }
@@ -1069,7 +1105,8 @@ int launchTicks(carl_env* e, int kind, const void* actions, int n)
                                  dim3(kContactBlock), 0, st, d, e->ws, e->contactScreen, r));
             CARL_MARK(launchTick(e, timed, CARL_KERNEL_CAR_ARENA, carArenaKernel, dim3(e->grid(cars, kTickBlock)),
                                  dim3(kTickBlock), 0, st, d, e->ws, kind, actions, tick, r));
-            CARL_MARK(launchTick(e, timed, CARL_KERNEL_BALL, ballKernel, dim3(e->grid(sims, kBallOwners)),
+            CARL_MARK(launchTick(e, timed, CARL_KERNEL_BALL, e->nativeRec ? ballNativeKernel : ballKernel,
+                                 dim3(e->grid(sims, kBallOwners)),
                                  dim3(kBallBlock), 0, st, d, tick, r));
             CARL_MARK(launchTick(e, timed, CARL_KERNEL_FINISH, finishKernel, dim3(e->grid(sims, spb)),
                                  dim3(spb * e->nCars), 0, st, d, spb, r));
@@ -1212,7 +1249,11 @@ int carl_env_create(int nSim, int nBlue, int nOrange, int seed, int frameskip, i
 
     carl::HostArena host;
     const std::string path = findArenaObj(libraryDir());
-    const std::string err = buildArena(path, host);
+    std::string err = buildArena(path, host);
+    // the native mesh metadata, when named (src/ArenaMesh.cu:69-99)
+    if (err.empty()) {
+        if (const char* meta = std::getenv("CARL_ARENA_METADATA")) err = readArenaMetadata(meta, host);
+    }
     if (!err.empty()) return fail(CARL_ERR_ARENA, err);
 
     carl_env* e = new carl_env();
@@ -1266,6 +1307,13 @@ int carl_env_create(int nSim, int nBlue, int nOrange, int seed, int frameskip, i
     rc = rc ? rc : devAlloc(&e->actions, nT * 7);
     rc = rc ? rc : devAlloc(&e->cactions, nT * 7);
     rc = rc ? rc : devAlloc(&e->ws, (size_t)kWsPlanes * tiledItems(e->nTotal));
+    if (!host.nativeRecords.empty()) {
+        rc = rc ? rc : devAlloc(&e->nativeRec, host.nativeRecords.size() / 4);
+        rc = rc ? rc : devAlloc(&e->ballScratch, (size_t)kNativeMaxContacts * kNativeSlotWords * nS);
+        if (!rc && hipMemcpy(e->nativeRec, host.nativeRecords.data(), host.nativeRecords.size() * sizeof(float),
+                             hipMemcpyHostToDevice) != hipSuccess)
+            rc = fail(CARL_ERR_RUNTIME, "hipMemcpy failed");
+    }
     if (rc) return bail(rc);
 
     std::vector<float4> ang(host.angles.size() / 3);
@@ -1517,6 +1565,7 @@ int carl_env_get_param(carl_env* e, int p, int* v)
     case CARL_PARAM_TICK_STREAMS: *v = e->tickStreams; break;
     case CARL_PARAM_CONTACT_SCREEN: *v = e->contactScreen; break;
     case CARL_PARAM_TICK_WINDOW: *v = e->windowSims; break;
+    case CARL_PARAM_NATIVE_ARENA: *v = e->nativeRec != nullptr; break;
     default: return fail(CARL_ERR_VALUE, "unknown parameter");
     }
     return CARL_OK;
@@ -1526,6 +1575,8 @@ int carl_env_enable_timing(carl_env* e, int enable)
 {
     CARL_TRY(checkEnv(e));
     HIP_TRY(hipStreamSynchronize(e->stream));
+    if ((enable & CARL_TIME_STAGES) && e->nativeRec)
+        return fail(CARL_ERR_VALUE, "the stage profile does not cover the native arena meshes");
     e->timing = enable & (CARL_TIME_TICKS | CARL_TIME_PACKING | CARL_TIME_STAGES);
     e->timedLaunches = 0;
     for (int k = 0; k < CARL_TICK_KERNELS; k++) {

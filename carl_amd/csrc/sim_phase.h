@@ -788,6 +788,274 @@ DI void solveBallContacts(BallBody& b, const BallContact* cs, int count, bool wa
     if (as > kBallMaxAng * kBallMaxAng) b.ang = b.ang * (kBallMaxAng * rsqrt_(as));
 }
 
+// ------------------------------------------- ball vs native arena meshes
+// With CARL_ARENA_METADATA the ball meets the arena as RocketSim's native
+// meshes do (BallArena/Contact.cuh:292-343, 406-470, 478-594): the native
+// triangles in Bullet units, visited in native order (mesh, then position
+// within the mesh), at most four contacts kept per mesh, and the four arena
+// planes as analytic contacts.  Up to kNativeMaxContacts contacts per ball
+// live in the environment's ball scratch, slot-major and field-major
+// ((slot * kNativeSlotWords + field) * nSim + sim): first each contact's
+// offset, normal and depth, then the solver's split row built from it.  One
+// lane serves one ball.
+
+constexpr int kNativeMaxContacts = 68;   // the reference's capacity: sixteen meshes of four and the planes
+constexpr int kNativeSlotWords = 10;
+
+struct NativeTri {
+    V3 v0, v1, v2;
+    int key, mesh, flags;
+};
+
+DI NativeTri loadNativeTri(const ArenaView& a, int idx)
+{
+    const float4* r = a.native + 4 * (size_t)idx;
+    const float4 r0 = r[0], r1 = r[1], r2 = r[2];
+    return NativeTri{ V3{ r0.x, r0.y, r0.z }, V3{ r1.x, r1.y, r1.z }, V3{ r2.x, r2.y, r2.z },
+                      (int)__float_as_uint(r0.w), (int)__float_as_uint(r1.w), (int)__float_as_uint(r2.w) };
+}
+
+DI float& nativeWord(const Dev& d, int sim, int slot, int field)
+{
+    return d.ballScratch[(size_t)(slot * kNativeSlotWords + field) * d.nSim + sim];
+}
+
+// sphere against one native triangle, all in Bullet units
+// (BallArena/Contact.cuh:292-343); reduction = relPos
+DI bool nativeSphereTriangle(V3 center, const NativeTri& t, BallContact& ct)
+{
+    constexpr float radius = kBallRadius * .02f;
+    constexpr float extent = radius + kBallArenaBreak * .02f;
+    const V3 e01 = t.v1 - t.v0, e02 = t.v2 - t.v0;
+    const V3 off = center - t.v0;
+    const V3 face = cross(e01, e02);
+    const float nl = lensq(face);
+    if (nl < 1e-14f) return false;
+    V3 n = face * (1.f / sqrtf(nl));
+    float plane = dot(off, n);
+    if (plane < 0.f) {
+        plane = -plane;
+        n = -n;
+    }
+    if (plane >= extent) return false;
+    const float gamma = dot(cross(e01, off), face) / nl;
+    const float beta = dot(cross(off, e02), face) / nl;
+    const float alpha = 1.f - gamma - beta;
+    const bool inside = alpha >= 0.f && alpha <= 1.f && beta >= 0.f && beta <= 1.f && gamma >= 0.f && gamma <= 1.f;
+    const V3 point = inside ? center - n * plane : closestOnTriangle(center, t.v0, t.v1, t.v2);
+    const V3 delta = center - point;
+    const float dsq = lensq(delta);
+    if (dsq >= extent * extent) return false;
+    const float dist = sqrtf(dsq);
+    ct.point = point;
+    ct.normal = dsq > kFltEps ? delta * (1.f / dist) : n;
+    ct.depth = dsq > kFltEps ? radius - dist : radius;
+    ct.relPos = (point - ct.normal * ct.depth) - center;
+    ct.reduction = ct.relPos;
+    return true;
+}
+
+// native internal-edge correction (BallArena/Contact.cuh:161-202): the edge
+// within 0.1 Bullet units of the contact point, its metadata flags choosing
+// the sides; the clamped normal is kept as the rotation leaves it
+DI void adjustNativeBallEdge(BallContact& ct, const NativeTri& t, V3 angles)
+{
+    const float maxSq = .1f * .1f;
+    int best = -1;
+    float bestSq = maxSq;
+#pragma unroll
+    for (int e = 0; e < 3; e++) {
+        if (fabsf(comp(angles, e)) >= kBoundaryEdge) continue;
+        const V3 s = e == 0 ? t.v0 : (e == 1 ? t.v1 : t.v2);
+        const V3 en = e == 0 ? t.v1 : (e == 1 ? t.v2 : t.v0);
+        const V3 edge = en - s;
+        const float u = clamp_(dot(ct.point - s, edge) / lensq(edge), 0.f, 1.f);
+        const float sq = lensq(ct.point - (s + edge * u));
+        if (sq < bestSq) { bestSq = sq; best = e; }
+    }
+    if (best < 0) return;
+    const V3 face = normalize(cross(t.v1 - t.v0, t.v2 - t.v0));
+    const V3 s = sel(best == 0, t.v0, sel(best == 1, t.v1, t.v2));
+    const V3 en = sel(best == 0, t.v1, sel(best == 1, t.v2, t.v0));
+    const V3 edgeDir = normalize(s - en);
+    const float angle = comp(angles, best);
+    bool concave = angle == 0.f;
+    if (!concave) {
+        const float sign = (t.flags & (1 << best)) ? 1.f : -1.f;
+        V3 other = rodrigues(face, edgeDir, angle);
+        if (t.flags & (1 << (best + 3))) other = -other;
+        concave = dot(ct.normal, face * sign) < 0.f && dot(ct.normal, other * sign) < 0.f;
+        if (!concave) {
+            V3 cl;
+            if (clampEdgeNormal(edgeDir, face * sign, ct.normal, angle, cl) && dot(cl, face) > 0.f) ct.normal = cl;
+        }
+    }
+    if (concave && dot(face, ct.normal) >= 0.f) ct.normal = face;
+}
+
+// a finished mesh group's contacts into their slots, back in Unreal units
+DI void storeNativeGroup(const Dev& d, int sim, int base, int n, const BallContact* cs)
+{
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        if (i >= n) break;
+        const float v[7] = { cs[i].relPos.x * 50.f, cs[i].relPos.y * 50.f, cs[i].relPos.z * 50.f, cs[i].normal.x,
+                             cs[i].normal.y,        cs[i].normal.z,        cs[i].depth * 50.f };
+#pragma unroll
+        for (int f = 0; f < 7; f++) nativeWord(d, sim, base + i, f) = v[f];
+    }
+}
+
+// The native contacts of a ball centred at `center` into the ball's slots;
+// returns their count.  The reference merges its cells' lists, sorted by
+// order key (mesh * 10000 + order), and visits each distinct triangle once
+// in that order; here each pass over the overlapped cells finds the
+// smallest (key, triangle) pair above the last one visited whose triangle
+// makes contact, the same sequence when keys are unique (equal keys, which
+// the reference leaves in std::sort's order, go by triangle index).  The
+// planes in reach are counted first; a contact that would need a slot past
+// the 68 less those is dropped (the reference writes past its array there).
+DI int gatherNativeBallContacts(const Dev& d, int sim, V3 center)
+{
+    // the arena planes: floor, ceiling, the two side walls (analytic)
+    const V3 normals[4] = { V3{ 0.f, 0.f, 1.f }, V3{ 0.f, 0.f, -1.f }, V3{ 1.f, 0.f, 0.f }, V3{ -1.f, 0.f, 0.f } };
+    const float offsets[4] = { 0.f, -2044.f, -4096.f, -4096.f };
+    float planeDepth[4];
+    int room = kNativeMaxContacts;
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        planeDepth[p] = kBallRadius - (dot(normals[p], center) - offsets[p]);
+        room -= planeDepth[p] > -kBallArenaBreak;
+    }
+    const float ext = kBallRadius + kBallArenaBreak;
+    int lo[3], hi[3];
+    cellOf(center - ext, lo[0], lo[1], lo[2]);
+    cellOf(center + ext, hi[0], hi[1], hi[2]);
+    const V3 cb = center * .02f;
+    BallContact cs[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) cs[k] = BallContact{ kZero, kZero, kZero, 0.f, kZero };
+    int count = 0, local = 0, mesh = -1, base = 0;
+    constexpr long long kNone = 0x7fffffffffffffffLL;
+    long long last = -kNone - 1;
+    for (;;) {
+        long long next = kNone;
+        for (int z = lo[2]; z <= hi[2]; z++)
+            for (int y = lo[1]; y <= hi[1]; y++)
+                for (int x = lo[0]; x <= hi[0]; x++) {
+                    const int cell = flatCell(x, y, z);
+                    const int e = d.arena.cellStart[cell + 1];
+                    for (int r = d.arena.cellStart[cell]; r < e; r++) {
+                        const int idx = (int)(__float_as_uint(d.arena.rec[4 * (size_t)r + 3].w) & ~kPlaneFlag);
+                        const NativeTri t = loadNativeTri(d.arena, idx);
+                        const long long k = (long long)t.key * 4294967296LL + idx;
+                        if (k <= last || k >= next || t.mesh < 0) continue;
+                        BallContact ct;
+                        if (nativeSphereTriangle(cb, t, ct)) next = k;
+                    }
+                }
+        if (next == kNone) break;
+        last = next;
+        const int idx = (int)(next & 0xffffffffLL);
+        const NativeTri t = loadNativeTri(d.arena, idx);
+        BallContact ct;
+        nativeSphereTriangle(cb, t, ct);
+        if (t.mesh != mesh) {
+            storeNativeGroup(d, sim, base, local, cs);
+            base = count;
+            local = 0;
+            mesh = t.mesh;
+        }
+        int slot;
+        if (local < 4) {
+            if (count == room) continue;
+            slot = local++;
+            count++;
+        } else {
+            slot = ballReplacement(cs, ct);
+        }
+        const float4 a = d.arena.native[4 * (size_t)idx + 3];
+        adjustNativeBallEdge(ct, t, V3{ a.x, a.y, a.z });
+#pragma unroll
+        for (int i = 0; i < 4; i++) cs[i] = sel(i == slot, ct, cs[i]);
+    }
+    storeNativeGroup(d, sim, base, local, cs);
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        const float depth = planeDepth[p];
+        if (!(depth > -kBallArenaBreak)) continue;
+        const V3 rel = normals[p] * -kBallRadius;
+        const float v[7] = { rel.x, rel.y, rel.z, normals[p].x, normals[p].y, normals[p].z, depth };
+#pragma unroll
+        for (int f = 0; f < 7; f++) nativeWord(d, sim, count, f) = v[f];
+        count++;
+    }
+    return count;
+}
+
+// The averaged-contact solve of solveBallContacts over the ball's stored
+// native contacts; each slot's contact is replaced by its split row (axis,
+// relative cross, jacInv, rhsPen, applied push).
+DI void solveNativeBallContacts(const Dev& d, int sim, BallBody& b, int count, bool wasHit)
+{
+    if (count == 0) return;
+    V3 totalN = kZero;
+    float totalR = 0.f;
+    const bool doSplit = !wasHit || count != 1 || nativeWord(d, sim, 0, 5) < 0.999f;
+    for (int i = 0; i < count; i++) {
+        const V3 rel{ nativeWord(d, sim, i, 0), nativeWord(d, sim, i, 1), nativeWord(d, sim, i, 2) };
+        const V3 n{ nativeWord(d, sim, i, 3), nativeWord(d, sim, i, 4), nativeWord(d, sim, i, 5) };
+        const float depth = nativeWord(d, sim, i, 6);
+        const BRow r = ballNormalRow(b, n, depth, rel, doSplit);
+        totalN = totalN + n;
+        totalR += sqrtf(lensq(rel));
+        const float v[9] = { r.axis.x, r.axis.y, r.axis.z, r.relCross.x, r.relCross.y, r.relCross.z,
+                             r.jacInv, r.rhsPen,  0.f };
+#pragma unroll
+        for (int f = 0; f < 9; f++) nativeWord(d, sim, i, f) = v[f];
+    }
+    const float fc = (float)count;
+    const V3 avgN = totalN * (1.f / fc);
+    const V3 avgRel = avgN * (-totalR / fc);
+    const float avgDepth = -totalR / fc;
+    BRow nr = ballNormalRow(b, avgN, avgDepth, avgRel, false);
+    const V3 pv = b.vel + cross(b.ang, avgRel);
+    V3 tan = pv - avgN * dot(avgN, pv);
+    const float tl = lensq(tan);
+    tan = tl > 1e-8f ? tan * rsqrt_(tl) : fallbackTangent(avgN);
+    BRow fr = ballRow(tan, avgRel);
+    fr.rhs = -bRowVel(fr, b.vel, b.ang) * fr.jacInv;
+    for (int it = 0; it < kSolverIters; it++) {
+        for (int i = 0; i < count; i++) {
+            BRow r;
+            r.rhsPen = nativeWord(d, sim, i, 7);
+            if (r.rhsPen == 0.f) continue;
+            r.axis = V3{ nativeWord(d, sim, i, 0), nativeWord(d, sim, i, 1), nativeWord(d, sim, i, 2) };
+            r.relCross = V3{ nativeWord(d, sim, i, 3), nativeWord(d, sim, i, 4), nativeWord(d, sim, i, 5) };
+            r.jacInv = nativeWord(d, sim, i, 6);
+            r.appliedPush = nativeWord(d, sim, i, 8);
+            const float imp = pgsLower(r.rhsPen, r.jacInv, bRowVel(r, b.pushVel, b.pushAng), 0.f, r.appliedPush);
+            nativeWord(d, sim, i, 8) = r.appliedPush;
+            ballPush(b, r, imp, true);
+        }
+    }
+    for (int it = 0; it < kSolverIters; it++) {
+        const float ni = pgsLower(nr.rhs, nr.jacInv, bRowVel(nr, b.dVel, b.dAng), 0.f, nr.applied);
+        ballPush(b, nr, ni, false);
+        const float maxImp = kBallFriction * nr.applied;
+        if (maxImp > 0.f) {
+            const float fi = pgsClamp(fr.rhs, fr.jacInv, bRowVel(fr, b.dVel, b.dAng), -maxImp, maxImp, fr.applied);
+            ballPush(b, fr, fi, false);
+        }
+    }
+    b.vel = b.vel + b.dVel;
+    b.ang = b.ang + b.dAng;
+    const float ss = lensq(b.vel);
+    if (ss > kBallMaxSpeed * kBallMaxSpeed) b.vel = b.vel * (kBallMaxSpeed * rsqrt_(ss));
+    const float as = lensq(b.ang);
+    if (as > kBallMaxAng * kBallMaxAng) b.ang = b.ang * (kBallMaxAng * rsqrt_(as));
+}
+
 // --------------------------------------------------------------- ball vs car
 
 struct BCRow {
@@ -932,9 +1200,10 @@ DI bool ballSleeping(const Dev& d, int sim)
     return lensq(d.sv(CARL_SIM_BALL_VEL, sim)) == 0.f && lensq(d.sv(CARL_SIM_BALL_ANG, sim)) == 0.f;
 }
 
-// cs/count: the arena contacts of the exported ball position (unused when
-// the ball sleeps)
-DI void ballTick(const Dev& d, int sim, int tick, const BallContact* cs, int count)
+// solveArena(body, wasHit): the ball-arena solve at the exported ball
+// position (not called when the ball sleeps)
+template <class SolveArena>
+DI void ballTickWith(const Dev& d, int sim, int tick, SolveArena solveArena)
 {
     const V3 ballVel = d.sv(CARL_SIM_BALL_VEL, sim), ballAng = d.sv(CARL_SIM_BALL_ANG, sim);
     const bool sleeping = lensq(ballVel) == 0.f && lensq(ballAng) == 0.f;
@@ -959,7 +1228,7 @@ DI void ballTick(const Dev& d, int sim, int tick, const BallContact* cs, int cou
         BallBody b;
         b.vel = preVel; b.velNoExt = velNoExt; b.ang = ballAng;
         b.dVel = kZero; b.dAng = kZero; b.pushVel = kZero; b.pushAng = kZero;
-        solveBallContacts(b, cs, count, hit);
+        solveArena(b, hit);
         d.ssetv(CARL_SIM_BALL_VEL, sim, b.vel);
         d.ssetv(CARL_SIM_BALL_ANG, sim, b.ang);
         pushVel = b.pushVel;
@@ -996,6 +1265,22 @@ DI void ballTick(const Dev& d, int sim, int tick, const BallContact* cs, int cou
     else d.sseti(CARL_SIM_ORANGE_SCORE, sim, d.si(CARL_SIM_ORANGE_SCORE, sim) + 1);
     d.sseti(CARL_SIM_LAST_SCORER, sim, scorer);
     d.sseti(CARL_SIM_GOAL_TICK, sim, tick);
+}
+
+// cs/count: the arena contacts of the exported ball position (unused when
+// the ball sleeps)
+DI void ballTick(const Dev& d, int sim, int tick, const BallContact* cs, int count)
+{
+    ballTickWith(d, sim, tick, [&](BallBody& b, bool hit) { solveBallContacts(b, cs, count, hit); });
+}
+
+// the same with the native arena meshes
+DI void nativeBallTick(const Dev& d, int sim, int tick)
+{
+    ballTickWith(d, sim, tick, [&](BallBody& b, bool hit) {
+        const int n = gatherNativeBallContacts(d, sim, d.sv(CARL_SIM_BALL_POS, sim));
+        solveNativeBallContacts(d, sim, b, n, hit);
+    });
 }
 
 // ------------------------------------------------------------ finish, pads

@@ -42,6 +42,7 @@ struct ArenaView {
     const float4* fineRec;   // 4 per ball-grid reference (record layout)
     const float4* fineAux;   // per ball-grid reference: edge angles xyz, packed broadphase registration range
     const int* fineStart;    // kFineCells + 1 offsets into fineRec (in references)
+    const float4* native;    // 4 per triangle, native mesh metadata (arena.h); null without it
 };
 
 struct Tri {
@@ -94,6 +95,7 @@ struct Dev {
     uint32_t* sim;
     int nSim, nBlue, nCars, nTotal, seed;
     ArenaView arena;
+    float* ballScratch;  // native arena meshes only: the balls' contacts and rows (sim_phase.h)
 
     // Raw buffer resources over the two blocks (dword 3: the gfx9 raw-buffer
     // format); accesses past the end read 0 and store nothing.

@@ -122,9 +122,11 @@ enum {
     CARL_PARAM_CONTACT_SCREEN = 12, /* 1: the contact search drops (car, triangle) pairs its float tests
                                       provably reject before running them; 0: it runs them on every pair.
                                       Results are identical; no reference counterpart (default 1) */
-    CARL_PARAM_TICK_WINDOW = 13    /* > 0: all ticks of a step in one launch per partition, this many
+    CARL_PARAM_TICK_WINDOW = 13,   /* > 0: all ticks of a step in one launch per partition, this many
                                       simulations per workgroup (at most 128 cars; default 64); 0: four phase kernels
                                       per tick.  Results are identical; no reference counterpart */
+    CARL_PARAM_NATIVE_ARENA = 14   /* read-only: 1 when the environment was created with native mesh
+                                      metadata (the reference's ArenaMesh::hasNativeMetadata) */
 };
 
 /* ---- persistent state layout (export / import) ------------------------
@@ -225,7 +227,17 @@ typedef struct carl_env carl_env;
 
 /* Loads the arena mesh (env CARL_ARENA_OBJ, else carl_amd/assets/arena.obj next
  * to the library), allocates device state, resets every simulation to a
- * kickoff and packs the initial outputs.  frameskip >= 1. */
+ * kickoff and packs the initial outputs.  frameskip >= 1.
+ * When the environment variable CARL_ARENA_METADATA is set, its file holds
+ * RocketSim's native mesh metadata for every triangle (the text that
+ * tools/arena_metadata.py writes: the triangle count, then per triangle
+ * "mesh order angle0 angle1 angle2 flags v0x v0y v0z v1x v1y v1z v2x v2y v2z"
+ * with the vertices in Bullet units, src/ArenaMesh.cu:69-99), and the ball
+ * meets the arena as the native meshes do (BallArena/Contact.cuh:292-594).
+ * A count other than the mesh's triangle count (an unreadable file reads as
+ * count 0) fails with CARL_ERR_ARENA "CARL arena metadata triangle count
+ * mismatch"; a file that ends early or holds a non-number fails with
+ * "Invalid CARL arena metadata". */
 int carl_env_create(int n_sim, int n_blue, int n_orange, int seed, int frameskip,
                     int flags, carl_env** out);
 int carl_env_destroy(carl_env* env);

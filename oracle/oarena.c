@@ -9,6 +9,7 @@
  *   48x48x10 grid, cells [cell(min)-1, cell(max)]
  *                                      include/Arena/BroadPhaseGrid.cuh:11-78
  *   signed edge angles                 include/Arena/EdgeInfo.cuh:60-125
+ *   native mesh metadata               src/ArenaMesh.cu:69-124
  */
 #include <stdio.h>
 #include <stdlib.h>
@@ -68,6 +69,7 @@ void oarena_free(OArena* a)
     if (!a) return;
     free(a->verts); free(a->tris); free(a->norms); free(a->aabbMin);
     free(a->aabbMax); free(a->angs); free(a->cellTris);
+    free(a->nkey); free(a->nmesh); free(a->nflags); free(a->nverts); free(a->nangs); free(a->ballTris);
     free(a);
 }
 
@@ -225,4 +227,69 @@ OArena* oarena_load(const char* path, char* err, int errLen)
     free(table);
     if (fail) { set_err(err, errLen, fail); oarena_free(a); return NULL; }
     return a;
+}
+
+/* src/ArenaMesh.cu:69-99: the count, then per triangle mesh, order, three
+ * edge angles, flags and three vertices, read one after another; the read
+ * state is checked after the last triangle only.  A file that does not open
+ * reads as count 0.  Then (:109-124) each cell's ball list is sorted by the
+ * order key; triangles of equal keys, whose order the reference leaves to
+ * std::sort, go by triangle index here. */
+typedef struct { int key, tri; } BallKey;
+
+static int ball_key_cmp(const void* x, const void* y)
+{
+    const BallKey* a = (const BallKey*)x;
+    const BallKey* b = (const BallKey*)y;
+    if (a->key != b->key) return a->key < b->key ? -1 : 1;
+    return a->tri < b->tri ? -1 : (a->tri > b->tri);
+}
+
+int oarena_load_metadata(OArena* a, const char* path, char* err, int errLen)
+{
+    FILE* f = fopen(path, "r");
+    int count = 0;
+    if (!f || fscanf(f, "%d", &count) != 1) count = 0;
+    if (count != a->nTris) {
+        if (f) fclose(f);
+        set_err(err, errLen, "CARL arena metadata triangle count mismatch");
+        return 0;
+    }
+    const int n = a->nTris;
+    a->nkey = (int*)calloc((size_t)n, sizeof(int));
+    a->nmesh = (int*)calloc((size_t)n, sizeof(int));
+    a->nflags = (int*)calloc((size_t)n, sizeof(int));
+    a->nverts = (V3*)calloc(3 * (size_t)n, sizeof(V3));
+    a->nangs = (V3*)calloc((size_t)n, sizeof(V3));
+    int ok = 1;
+    for (int t = 0; t < n && ok; t++) {
+        int mesh, order, flags;
+        float ax, ay, az, v[9];
+        ok = fscanf(f, "%d %d %f %f %f %d", &mesh, &order, &ax, &ay, &az, &flags) == 6;
+        for (int k = 0; k < 9 && ok; k++) ok = fscanf(f, "%f", &v[k]) == 1;
+        if (!ok) break;
+        /* mesh * 10000 + order in 32-bit arithmetic */
+        a->nkey[t] = (int)((uint32_t)mesh * 10000u + (uint32_t)order);
+        a->nmesh[t] = mesh;
+        a->nflags[t] = flags;
+        a->nangs[t] = v3(ax, ay, az);
+        for (int k = 0; k < 3; k++) a->nverts[3 * t + k] = v3(v[3 * k], v[3 * k + 1], v[3 * k + 2]);
+    }
+    fclose(f);
+    if (!ok) {
+        set_err(err, errLen, "Invalid CARL arena metadata");
+        return 0;
+    }
+    const int refs = a->cellPrefix[N_CELLS];
+    a->ballTris = (int*)malloc(sizeof(int) * (size_t)(refs ? refs : 1));
+    BallKey* keys = (BallKey*)malloc(sizeof(BallKey) * (size_t)(refs ? refs : 1));
+    for (int r = 0; r < refs; r++) { keys[r].tri = a->cellTris[r]; keys[r].key = a->nkey[a->cellTris[r]]; }
+    for (int c = 0; c < N_CELLS; c++) {
+        const int lo = a->cellPrefix[c], cnt = a->cellPrefix[c + 1] - lo;
+        if (cnt > 1) qsort(keys + lo, (size_t)cnt, sizeof(BallKey), ball_key_cmp);
+    }
+    for (int r = 0; r < refs; r++) a->ballTris[r] = keys[r].tri;
+    free(keys);
+    a->native = 1;
+    return 1;
 }

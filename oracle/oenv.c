@@ -227,6 +227,12 @@ OEnv* oracle_create(int nSim, int nBlue, int nOrange, int seed, int frameskip, i
 {
     OArena* a = oarena_load(objPath, err, errLen);
     if (!a) return NULL;
+    /* native mesh metadata, when named (src/ArenaMesh.cu:69-99) */
+    const char* meta = getenv("CARL_ARENA_METADATA");
+    if (meta && !oarena_load_metadata(a, meta, err, errLen)) {
+        oarena_free(a);
+        return NULL;
+    }
     OEnv* e = (OEnv*)calloc(1, sizeof(OEnv));
     OWorld* w = &e->w;
     w->nSim = nSim; w->nBlue = nBlue; w->nOrange = nOrange; w->nCars = nBlue + nOrange;

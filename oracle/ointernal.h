@@ -271,6 +271,16 @@ typedef struct {
     V3* angs;         /* signed edge angle per triangle edge slot */
     int* cellTris;    /* per-cell triangle lists, ascending */
     int cellPrefix[N_CELLS + 1];
+    /* native mesh metadata (CARL_ARENA_METADATA), else native == 0 and the
+     * arrays are NULL: per triangle the order key (mesh * 10000 + order),
+     * mesh, edge flags, three vertices in Bullet units, three edge angles */
+    int native;
+    int* nkey;
+    int* nmesh;
+    int* nflags;
+    V3* nverts;
+    V3* nangs;
+    int* ballTris;    /* per-cell lists again, sorted by (order key, triangle) */
 } OArena;
 
 typedef struct {
@@ -295,6 +305,7 @@ O_INLINE float susp_scale(int w) { return w < 2 ? K_SUSP_SCALE_FRONT : K_SUSP_SC
 
 /* arena.c */
 OArena* oarena_load(const char* path, char* err, int errLen);
+int oarena_load_metadata(OArena* a, const char* path, char* err, int errLen);
 void oarena_free(OArena* a);
 void oarena_cell3(V3 p, int* cx, int* cy, int* cz);
 int oarena_flat(int cx, int cy, int cz);

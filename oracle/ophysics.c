@@ -1780,10 +1780,122 @@ static void adjust_ball_edge(OBallContact* ct, V3 point, V3 t0, V3 t1, V3 t2, V3
     if (clamp_normal(edgeAxis, nA, ct->normal, angle, &cl) && vdot(cl, face) > 0.f) ct->normal = vnorm(cl);
 }
 
-/* include/Physics/BallArena/Contact.cuh:513-594, default (non-native) branch:
- * triangles of the overlapped cells merged in ascending index order. */
+/* include/Physics/BallArena/Contact.cuh:292-343: the sphere against one
+ * native triangle, centre and vertices in Bullet units */
+static int native_sphere_triangle(OBallContact* ct, V3 center, V3 t0, V3 t1, V3 t2)
+{
+    const float radius = K_BALL_RADIUS * .02f;
+    const float extent = radius + K_BALL_ARENA_BREAK * .02f;
+    const V3 e01 = vsub(t1, t0), e02 = vsub(t2, t0), off = vsub(center, t0);
+    const V3 face = vcross(e01, e02);
+    const float nl = vlensq(face);
+    if (nl < 1e-14f) return 0;
+    V3 n = vscale(face, 1.f / sqrtf(nl));
+    float plane = vdot(off, n);
+    if (plane < 0.f) { plane = -plane; n = vneg(n); }
+    if (plane >= extent) return 0;
+    const float gamma = vdot(vcross(e01, off), face) / nl;
+    const float beta = vdot(vcross(off, e02), face) / nl;
+    const float alpha = 1.f - gamma - beta;
+    const int inside = alpha >= 0.f && alpha <= 1.f && beta >= 0.f && beta <= 1.f && gamma >= 0.f && gamma <= 1.f;
+    ct->point = inside ? vsub(center, vscale(n, plane)) : closest_on_triangle(center, t0, t1, t2);
+    const V3 delta = vsub(center, ct->point);
+    const float dsq = vlensq(delta);
+    if (dsq >= extent * extent) return 0;
+    const float dist = sqrtf(dsq);
+    ct->normal = dsq > K_FLT_EPS ? vscale(delta, 1.f / dist) : n;
+    ct->depth = dsq > K_FLT_EPS ? radius - dist : radius;
+    ct->relPos = vsub(vsub(ct->point, vscale(ct->normal, ct->depth)), center);
+    ct->reductionPos = ct->relPos;
+    return 1;
+}
+
+/* include/Physics/BallArena/Contact.cuh:161-202: the native internal-edge
+ * correction, sides chosen by the metadata flags (bit e: face side of edge e,
+ * bit e + 3: the neighbour's normal reversed) */
+static void adjust_native_ball_edge(OBallContact* ct, V3 t0, V3 t1, V3 t2, V3 angles, int flags, float edgeDistance)
+{
+    const V3 vs[3] = { t0, t1, t2 };
+    int best = -1;
+    float bestSq = edgeDistance * edgeDistance;
+    for (int e = 0; e < 3; e++) {
+        if (fabsf(vget(angles, e)) >= K_BOUNDARY_EDGE_ANGLE) continue;
+        const V3 st = vs[e], en = vs[(e + 1) % 3];
+        const V3 edge = vsub(en, st);
+        const float t = o_clamp(vdot(vsub(ct->point, st), edge) / vlensq(edge), 0.f, 1.f);
+        const float sq = vlensq(vsub(ct->point, vadd(st, vscale(edge, t))));
+        if (sq < bestSq) { bestSq = sq; best = e; }
+    }
+    if (best < 0) return;
+    const V3 face = vnorm(vcross(vsub(t1, t0), vsub(t2, t0)));
+    const V3 edgeDir = vnorm(vsub(vs[best], vs[(best + 1) % 3]));
+    const float angle = vget(angles, best);
+    int concave = angle == 0.f;
+    if (!concave) {
+        const float sign = (flags & (1 << best)) ? 1.f : -1.f;
+        V3 other = o_rotate_axis(face, edgeDir, angle);
+        if (flags & (1 << (best + 3))) other = vneg(other);
+        concave = vdot(ct->normal, vscale(face, sign)) < 0.f && vdot(ct->normal, vscale(other, sign)) < 0.f;
+        if (!concave) {
+            V3 cl;
+            if (clamp_normal(edgeDir, vscale(face, sign), ct->normal, angle, &cl) && vdot(cl, face) > 0.f)
+                ct->normal = cl;
+        }
+    }
+    if (concave && vdot(face, ct->normal) >= 0.f) ct->normal = face;
+}
+
+/* the arena planes of the native branch: floor, ceiling, side walls */
+static const V3 k_plane_normals[4] = { { 0.f, 0.f, 1.f }, { 0.f, 0.f, -1.f }, { 1.f, 0.f, 0.f }, { -1.f, 0.f, 0.f } };
+static const float k_plane_offsets[4] = { 0.f, -2044.f, -4096.f, -4096.f };
+
+static float native_plane_depth(V3 center, int p)
+{
+    return K_BALL_RADIUS - (vdot(k_plane_normals[p], center) - k_plane_offsets[p]);
+}
+
+static int count_native_planes(V3 center)
+{
+    int n = 0;
+    for (int p = 0; p < 4; p++) n += native_plane_depth(center, p) > -K_BALL_ARENA_BREAK;
+    return n;
+}
+
+/* include/Physics/BallArena/Contact.cuh:478-511: native contacts back to
+ * Unreal units, then the four arena planes as analytic contacts */
+static int finish_native_ball_contacts(OBallContact* cs, int count, V3 center)
+{
+    const V3* normals = k_plane_normals;
+    for (int i = 0; i < count; i++) {
+        cs[i].point = vscale(cs[i].point, 50.f);
+        cs[i].relPos = vscale(cs[i].relPos, 50.f);
+        cs[i].depth *= 50.f;
+    }
+    for (int p = 0; p < 4; p++) {
+        const float depth = native_plane_depth(center, p);
+        if (depth > -K_BALL_ARENA_BREAK) {
+            OBallContact* c = &cs[count++];
+            memset(c, 0, sizeof *c);
+            c->point = vsub(center, vscale(normals[p], K_BALL_RADIUS - depth));
+            c->relPos = vscale(normals[p], -K_BALL_RADIUS);
+            c->normal = normals[p];
+            c->depth = depth;
+            c->tri = -1;
+        }
+    }
+    return count;
+}
+
+/* include/Physics/BallArena/Contact.cuh:513-594: the cells' ball lists merged
+ * in order (by triangle index, or with native metadata by (order key,
+ * triangle)), each distinct triangle once; at most four contacts kept per
+ * native mesh.  With metadata a contact that would need a slot past the 68
+ * less the planes in reach is dropped: the reference writes past its array
+ * there. */
 static int gather_ball_contacts(const OArena* A, V3 center, OBallContact* cs)
 {
+    const int native = A->native;
+    const int* lists = native ? A->ballTris : A->cellTris;
     const float ext = K_BALL_RADIUS + K_BALL_ARENA_BREAK;
     int lo[3], hi[3];
     oarena_cell3(vsubs(center, ext), &lo[0], &lo[1], &lo[2]);
@@ -1798,34 +1910,54 @@ static int gather_ball_contacts(const OArena* A, V3 center, OBallContact* cs)
                 cells++;
             }
     int count = 0, mesh = -1, base = 0, localCount = 0, lastTri = -1;
+    int room = MAX_BALL_CONTACTS;
+    if (native) room -= count_native_planes(center);
     for (;;) {
-        int sel = -1, tri = -1, key = 2147483647;
+        int sel = -1, tri = -1;
+        long long key = 0x7fffffffffffffffLL;
         for (int c = 0; c < cells; c++) {
             if (cursor[c] >= end[c]) continue;
-            const int t = A->cellTris[cursor[c]];
-            if (t < key) { key = t; sel = c; tri = t; }
+            const int t = lists[cursor[c]];
+            const long long k = native ? (long long)A->nkey[t] * 4294967296LL + t : t;
+            if (k < key) { key = k; sel = c; tri = t; }
         }
         if (sel >= 0) cursor[sel]++;
         if (tri < 0) break;
         if (tri == lastTri) continue;
         lastTri = tri;
-        const int current = 0;
+        const int current = native ? A->nmesh[tri] : 0;
+        if (native && current < 0) continue;
         OBallContact ct;
         memset(&ct, 0, sizeof ct);
         ct.tri = -1;
-        const V3 t0 = A->verts[A->tris[3 * tri]], t1 = A->verts[A->tris[3 * tri + 1]], t2 = A->verts[A->tris[3 * tri + 2]];
-        if (!sphere_triangle(&ct, center, K_BALL_RADIUS, t0, t1, t2)) continue;
-        ct.reductionPos = ct.relPos;
+        V3 t0, t1, t2;
+        if (native) {
+            t0 = A->nverts[3 * tri]; t1 = A->nverts[3 * tri + 1]; t2 = A->nverts[3 * tri + 2];
+            if (!native_sphere_triangle(&ct, vscale(center, .02f), t0, t1, t2)) continue;
+        } else {
+            t0 = A->verts[A->tris[3 * tri]]; t1 = A->verts[A->tris[3 * tri + 1]]; t2 = A->verts[A->tris[3 * tri + 2]];
+            if (!sphere_triangle(&ct, center, K_BALL_RADIUS, t0, t1, t2)) continue;
+            ct.reductionPos = ct.relPos;
+        }
         ct.tri = tri;
         if (current != mesh) { base = count; localCount = 0; mesh = current; }
         int slot;
-        if (localCount < 4) { slot = localCount++; count++; }
+        if (localCount < 4) {
+            if (count == room) continue;
+            slot = localCount++;
+            count++;
+        }
         else slot = ball_replacement(cs + base, &ct);
-        adjust_ball_edge(&ct, ct.point, t0, t1, t2, A->angs[tri]);
-        ct.point = vadd(vadd(center, ct.relPos), vscale(ct.normal, ct.depth));
+        if (native) {
+            adjust_native_ball_edge(&ct, t0, t1, t2, A->nangs[tri], A->nflags[tri], .1f);
+            ct.point = vadd(vadd(vscale(center, .02f), ct.relPos), vscale(ct.normal, ct.depth));
+        } else {
+            adjust_ball_edge(&ct, ct.point, t0, t1, t2, A->angs[tri]);
+            ct.point = vadd(vadd(center, ct.relPos), vscale(ct.normal, ct.depth));
+        }
         cs[base + slot] = ct;
     }
-    return count;
+    return native ? finish_native_ball_contacts(cs, count, center) : count;
 }
 
 typedef struct { V3 pos, vel, velNoExt, ang, deltaVel, deltaAng, pushVel, pushAng; } OBallBody;
