@@ -266,10 +266,12 @@ std::string buildArena(const std::string& objPath, HostArena& out)
                               (float)s1, (float)s2, (float)s3, (float)epsEdge };
         std::memcpy(&screen[16 * (size_t)t], f, sizeof f);
     }
-    // ball candidate grid.  A ball only tests triangles registered in the
-    // broadphase cells its box overlaps; each reference carries the
+    // ball candidate grid, also the cars' contact-search lists.  A ball only
+    // tests triangles registered in the broadphase cells its box overlaps, a
+    // car those of its own broadphase cell; each reference carries the
     // triangle's edge angles and its registration range (x0 x1 y0 y1 6 bits
-    // each, z0 z1 4 bits) so the ball can apply that rule itself.
+    // each, z0 z1 4 bits) so that either can apply its rule itself, and the
+    // triangle's contact-search screening data.
     {
         const double reach = (double)kBallRadius + (double)kBallArenaBreak + 1.0;
         auto fineRange = [&](int t, int (&a)[3], int (&b)[3]) {
@@ -294,6 +296,7 @@ std::string buildArena(const std::string& objPath, HostArena& out)
         const size_t nFine = (size_t)out.fineStart[kFineCells];
         out.fineRecords.assign(16 * nFine, 0.f);
         out.fineAux.assign(4 * nFine, 0.f);
+        out.fineBoxes.assign(16 * nFine, 0.f);
         std::fill(fcount.begin(), fcount.end(), 0);
         for (int t = 0; t < nTris; t++) {
             int a[3], b[3];
@@ -307,6 +310,7 @@ std::string buildArena(const std::string& objPath, HostArena& out)
                         const int c = x + kFineX * (y + kFineY * z);
                         const size_t f = (size_t)out.fineStart[c] + fcount[c]++;
                         std::memcpy(&out.fineRecords[16 * f], &out.triRecords[16 * (size_t)t], 16 * sizeof(float));
+                        std::memcpy(&out.fineBoxes[16 * f], &screen[16 * (size_t)t], 16 * sizeof(float));
                         std::memcpy(&out.fineAux[4 * f], &out.angles[3 * (size_t)t], 3 * sizeof(float));
                         std::memcpy(&out.fineAux[4 * f + 3], &reg, sizeof reg);
                     }

@@ -64,6 +64,7 @@ DI V3 boxAabbMin(V3 cen, Q4 rot)
 struct Broad {
     int start;
     int count;
+    int cell;   // the cell's coordinates, x | y << 6 | z << 12
 };
 
 // grid cell of the min corner of the swept (current + predicted) AABB
@@ -77,7 +78,7 @@ DI Broad broadphase(const Dev& d, V3 pos, V3 vel, V3 ang, V3 cen, Q4 rot)
     cellOf(swept, cx, cy, cz);
     const int cell = flatCell(cx, cy, cz);
     const int s = d.arena.cellStart[cell];
-    return Broad{ s, d.arena.cellStart[cell + 1] - s };
+    return Broad{ s, d.arena.cellStart[cell + 1] - s, cx | cy << 6 | cz << 12 };
 }
 
 // ------------------------------------------------------------------ raycast
@@ -966,7 +967,9 @@ constexpr int kContactOwners = 32;
 
 struct ContactLds {
     int excl[64];
-    int first[kContactOwners];   // first cell reference of the owner's run
+    int first[kContactOwners];   // first reference of the owner's run
+    int fine[kContactOwners];    // the run is a candidate-grid list (else a broadphase cell's)
+    int bcell[kContactOwners];   // the owner's broadphase cell, x | y << 6 | z << 12
     int satOn[kContactOwners];   // owner takes part in the car-arena search (not demoed)
     float rot[4][kContactOwners];
     float start[kWheels][3][kContactOwners];
@@ -1002,14 +1005,30 @@ DI V3 ownerDir(const ContactLds& L, int o)
 
 struct RefBox {
     float4 lo, hi, pl, sat;
+    bool live;   // an item of the owner's broadphase cell
 };
 
-// screening data of item q of owner o (reference 0 for lanes without an item)
+// Whether a triangle with packed registration range `reg` (x0 x1 y0 y1 6 bits
+// each, z0 z1 4 bits) is listed in the broadphase cell `bcell`.
+DI bool registeredIn(uint32_t reg, int bcell)
+{
+    const int x = bcell & 63, y = (bcell >> 6) & 63, z = bcell >> 12;
+    return (int)(reg & 63) <= x && x <= (int)((reg >> 6) & 63) && (int)((reg >> 12) & 63) <= y &&
+           y <= (int)((reg >> 18) & 63) && (int)((reg >> 24) & 15) <= z && z <= (int)(reg >> 28);
+}
+
+// screening data of item q of owner o (reference 0 for lanes without an
+// item).  An item of a candidate-grid run counts only when the triangle is
+// listed in the owner's broadphase cell: the reference tests exactly the
+// triangles of that cell.
 DI RefBox contactFetch(const Dev& d, const ContactLds& L, int o, int q, bool valid)
 {
     const int ref = valid ? L.first[o] + q : 0;
-    const float4* b = d.arena.box + 4 * (size_t)ref;
-    return RefBox{ b[0], b[1], b[2], b[3] };
+    const bool fine = L.fine[o] != 0;
+    const float4* b = (fine ? d.arena.fineBox : d.arena.box) + 4 * (size_t)ref;
+    bool live = valid;
+    if (fine) live = live && registeredIn(__float_as_uint(d.arena.fineAux[ref].w), L.bcell[o]);
+    return RefBox{ b[0], b[1], b[2], b[3], live };
 }
 
 DI void waveSync()
@@ -1053,7 +1072,7 @@ DI void contactScreen(ContactLds& L, const RefBox& b, int o, int q, int lane)
     const float sh = dot(vabs(n), (rhi - rlo) * 0.5f);
     const bool rayMiss = (gap > kGapSlack && cosDir * (gap - kGapSlack) > b.pl.z) || sc - sh > b.pl.w ||
                          sc + sh < -b.pl.w;
-    const bool keep = s4.z == 0.f || !(satMiss && rayMiss);
+    const bool keep = b.live && (s4.z == 0.f || !(satMiss && rayMiss));
     const unsigned long long m = __ballot(keep);
     const int n0 = L.candN;
     if (keep) L.candQ[n0 + __popcll(m & lanesBelow(lane))] = (o << 24) | q;
@@ -1077,7 +1096,9 @@ DI void contactHeavy(const Dev& d, ContactLds& L, int lane)
     bool hasContact = false;
     ManPt manPt{};   // this lane's contact as a manifold point
     if (active) {
-        const Tri t = loadTri(d.arena, L.first[o] + q);
+        const int ref = L.first[o] + q;
+        const bool fine = L.fine[o] != 0;
+        const Tri t = unpackTri((fine ? d.arena.fineRec : d.arena.rec) + 4 * (size_t)ref);
         const V3 dir = ownerDir(L, o);
         const V3 pv = cross(dir, t.e2);
         const float det = dot(t.e1, pv);
@@ -1138,7 +1159,7 @@ DI void contactHeavy(const Dev& d, ContactLds& L, int lane)
             if (triBestContact(lt, sat, near, L.nearN[o], c, value)) {
                 atomicMin(&L.bestKey[o], contactKey(value, q));
                 const Q4 rot{ L.rot[0][o], L.rot[1][o], L.rot[2][o], L.rot[3][o] };
-                const float4 ang = d.arena.refAng[L.first[o] + q];
+                const float4 ang = fine ? d.arena.fineAux[ref] : d.arena.refAng[ref];
                 adjustEdgeContact(lt, V3{ ang.x, ang.y, ang.z }, c);
                 manPt = ManPt{ c.carPos, ownerCen(L, o) + rotate(rot, c.arenaPos), rotate(rot, c.normal), -c.depth };
                 hasContact = true;
@@ -1180,12 +1201,15 @@ DI void contactDrain(const Dev& d, ContactLds& L, int lane, bool last)
 
 // Owner side, before the search: pose, rays and (with sat) the plane points
 // of the car-arena search into LDS.  Lanes past the owners only reset the queue.
-DI void contactPrepare(ContactLds& L, int lane, bool sat, V3 cen, Q4 rot, int first, bool screen)
+DI void contactPrepare(ContactLds& L, int lane, bool sat, V3 cen, Q4 rot, int first, bool fine, int bcell,
+                       bool screen)
 {
     if (lane == 0) L.candN = 0;
     if (lane >= kContactOwners) return;
     const V3 dir = -rotate(rot, kZ);
     L.first[lane] = first;
+    L.fine[lane] = fine;
+    L.bcell[lane] = bcell;
     L.satOn[lane] = sat;
     L.rot[0][lane] = rot.x; L.rot[1][lane] = rot.y; L.rot[2][lane] = rot.z; L.rot[3][lane] = rot.w;
     const V3 ax = rotate(rot, kX), ay = rotate(rot, kY), az = rotate(rot, kZ);

@@ -100,6 +100,16 @@ struct SimRange {
 constexpr int kContactBlock = 64;
 static_assert(kContactOwners <= kContactBlock, "owners are lanes of the block");
 
+// The candidate-grid lists reach kBallRadius + kBallArenaBreak + 1 uu past
+// their cell; every car test stays closer to the car's centre: the box's
+// corners, and the wheel rays' ends (the rays start at the anchors, in the
+// centre's plane, and run along the car's down axis).
+constexpr float kGridReach = kBallRadius + kBallArenaBreak + 1.f;
+constexpr float sq(float x) { return x * x; }
+static_assert(sq(kHalf.x) + sq(kHalf.y) + sq(kHalf.z) < sq(kGridReach), "car box beyond the candidate grid");
+static_assert(sq(kFrontX) + sq(kFrontY) + sq(kFrontRay + 1.f) < sq(kGridReach), "front rays beyond the grid");
+static_assert(sq(kBackX) + sq(kBackY) + sq(kBackRay + 1.f) < sq(kGridReach), "back rays beyond the grid");
+
 // The contact search of cars [car0, car0 + kContactOwners) (those below
 // carEnd) by one wave; L is that wave's own LDS.  Every lane of the wave calls
 // it; it synchronises the wave only.
@@ -110,18 +120,27 @@ DI void contactGroup(const Dev& d, uint32_t* __restrict__ ws, int screen, int ca
     const bool ok = lane < kContactOwners && car < carEnd;
     V3 cen = kZero;
     Q4 rot{ 0.f, 0.f, 0.f, 1.f };
-    Broad bp{ 0, 0 };
-    bool demoed = false;
+    Broad bp{ 0, 0, 0 };
+    bool demoed = false, fine = false;
+    int first = 0, count = 0;
     if (ok) {
         cen = d.cv(CARL_CAR_CEN, car);
         rot = d.cq(CARL_CAR_ROT, car);
         bp = broadphase(d, d.cv(CARL_CAR_POS, car), d.cv(CARL_CAR_VEL, car), d.cv(CARL_CAR_ANG, car), cen, rot);
         demoed = d.ci(CARL_CAR_DEMOED, car) != 0;
+        // the candidate-grid list of the cell holding the car's centre, when
+        // there is one (every triangle within ball reach + 1 uu of the cell,
+        // in ascending triangle order; the car's tests reach less far), else
+        // the broadphase cell's run
+        int fcell;
+        fine = ballGridCell(cen, fcell);
+        first = fine ? d.arena.fineStart[fcell] : bp.start;
+        count = fine ? d.arena.fineStart[fcell + 1] - first : bp.count;
     }
-    contactPrepare(L, lane, ok && !demoed, cen, rot, bp.start, screen != 0);
+    contactPrepare(L, lane, ok && !demoed, cen, rot, first, fine, bp.cell, screen != 0);
     waveSync();
     waveItemsDeep<Depth>(
-        bp.count, L.excl, [&](int o, int q, bool valid) { return contactFetch(d, L, o, q, valid); },
+        count, L.excl, [&](int o, int q, bool valid) { return contactFetch(d, L, o, q, valid); },
         [&](const RefBox& b, int o, int q, int) { contactScreen(L, b, o, q, lane); },
         [&](bool last) { contactDrain(d, L, lane, last); });
     waveSync();
@@ -709,13 +728,13 @@ __global__ __launch_bounds__(kContactBlock) void refreshKernel(Dev d, Selection 
     const bool active = car >= 0 && !d.ci(CARL_CAR_DEMOED, car);
     V3 cen = kZero;
     Q4 rot{ 0.f, 0.f, 0.f, 1.f };
-    Broad bp{ 0, 0 };
+    Broad bp{ 0, 0, 0 };
     if (active) {
         cen = d.cv(CARL_CAR_CEN, car);
         rot = d.cq(CARL_CAR_ROT, car);
         bp = broadphase(d, d.cv(CARL_CAR_POS, car), d.cv(CARL_CAR_VEL, car), d.cv(CARL_CAR_ANG, car), cen, rot);
     }
-    contactPrepare(L, lane, false, cen, rot, bp.start, screen != 0);
+    contactPrepare(L, lane, false, cen, rot, bp.start, false, bp.cell, screen != 0);
     __syncthreads();
     waveItemsPipelined(
         bp.count, L.excl, [&](int o, int q, bool valid) { return contactFetch(d, L, o, q, valid); },
@@ -903,6 +922,7 @@ struct carl_env {
     float4* refAng = nullptr;
     float4* fineRec = nullptr;
     float4* fineAux = nullptr;
+    float4* fineBox = nullptr;
     int* fineStart = nullptr;
     float *obs = nullptr, *tobs = nullptr, *state = nullptr, *tstate = nullptr, *rewards = nullptr;
     bool *dones = nullptr, *overtime = nullptr, *tovertime = nullptr;
@@ -942,7 +962,7 @@ struct carl_env {
     {
         Dev d;
         d.car = car; d.sim = sim; d.nSim = nSim; d.nBlue = nBlue; d.nCars = nCars; d.nTotal = nTotal; d.seed = seed;
-        d.arena = ArenaView{ rec, cellStart, angles, triRec, refBox, refAng, fineRec, fineAux, fineStart, nativeRec };
+        d.arena = ArenaView{ rec, cellStart, angles, triRec, refBox, refAng, fineRec, fineAux, fineBox, fineStart, nativeRec };
         d.ballScratch = ballScratch;
         return d;
     }
@@ -963,7 +983,7 @@ int devAlloc(T** p, size_t count)
 void freeAll(carl_env* e)
 {
     void* ptrs[] = { e->car, e->sim, e->rec, e->cellStart, e->angles, e->triRec, e->refBox, e->refAng, e->fineRec,
-                     e->fineAux, e->fineStart, e->obs, e->tobs, e->state, e->tstate, e->rewards, e->dones,
+                     e->fineAux, e->fineBox, e->fineStart, e->obs, e->tobs, e->state, e->tstate, e->rewards, e->dones,
                      e->overtime, e->tovertime, e->score, e->ticks, e->tscore, e->tticks, e->actions, e->cactions,
                      e->ws, e->prof, e->nativeRec, e->ballScratch };
     for (void* p : ptrs)
@@ -1291,6 +1311,7 @@ int carl_env_create(int nSim, int nBlue, int nOrange, int seed, int frameskip, i
     rc = rc ? rc : devAlloc(&e->refAng, host.refAngles.size() / 4);
     rc = rc ? rc : devAlloc(&e->fineRec, host.fineRecords.size() / 4);
     rc = rc ? rc : devAlloc(&e->fineAux, host.fineAux.size() / 4);
+    rc = rc ? rc : devAlloc(&e->fineBox, host.fineBoxes.size() / 4);
     rc = rc ? rc : devAlloc(&e->fineStart, host.fineStart.size());
     rc = rc ? rc : devAlloc(&e->obs, nT * e->obsDim);
     rc = rc ? rc : devAlloc(&e->tobs, nT * e->obsDim);
@@ -1331,6 +1352,8 @@ int carl_env_create(int nSim, int nBlue, int nOrange, int seed, int frameskip, i
                != hipSuccess
         || hipMemcpy(e->fineRec, host.fineRecords.data(), host.fineRecords.size() * sizeof(float),
                      hipMemcpyHostToDevice) != hipSuccess
+        || hipMemcpy(e->fineBox, host.fineBoxes.data(), host.fineBoxes.size() * sizeof(float), hipMemcpyHostToDevice)
+               != hipSuccess
         || hipMemcpy(e->fineAux, host.fineAux.data(), host.fineAux.size() * sizeof(float), hipMemcpyHostToDevice)
                != hipSuccess
         || hipMemcpy(e->fineStart, host.fineStart.data(), host.fineStart.size() * sizeof(int), hipMemcpyHostToDevice)

@@ -41,6 +41,7 @@ struct ArenaView {
     const float4* refAng;    // per cell reference: the triangle's signed edge angles (xyz)
     const float4* fineRec;   // 4 per ball-grid reference (record layout)
     const float4* fineAux;   // per ball-grid reference: edge angles xyz, packed broadphase registration range
+    const float4* fineBox;   // 4 per ball-grid reference: contact-search screening data (as box)
     const int* fineStart;    // kFineCells + 1 offsets into fineRec (in references)
     const float4* native;    // 4 per triangle, native mesh metadata (arena.h); null without it
 };
