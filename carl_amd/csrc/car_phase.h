@@ -959,45 +959,49 @@ constexpr float kRotErr = 100.f * 0x1p-24f;    // rotated vertex error per unit 
 constexpr float kRotErr2 = 2.f * kRotErr;      // the same for an edge (two vertices)
 constexpr float kHalfLen = 80.f;               // |kHalf| rounded up
 
-// Cars searched per wave (owner lanes 0..kContactOwners-1); the other lanes
-// only take part in the cooperative item loop.  Sizing the per-owner LDS for
-// the owners alone keeps the block's LDS small enough that the kernel's
-// occupancy is set by its registers.
+// Cars searched per wave (owner lanes 0..Owners-1); the other lanes only
+// take part in the cooperative item loop.  The per-owner LDS is sized for the
+// owners alone.  The contact kernel searches kContactOwners cars per wave,
+// which keeps its block's LDS small enough that its occupancy is set by its
+// registers; the tick-window kernel searches a whole wave of cars at once.
 constexpr int kContactOwners = 32;
 
-struct ContactLds {
+template <int Owners>
+struct ContactLdsT {
     int excl[64];
-    int first[kContactOwners];   // first reference of the owner's run
-    int fine[kContactOwners];    // the run is a candidate-grid list (else a broadphase cell's)
-    int bcell[kContactOwners];   // the owner's broadphase cell, x | y << 6 | z << 12
-    int satOn[kContactOwners];   // owner takes part in the car-arena search (not demoed)
-    float rot[4][kContactOwners];
-    float start[kWheels][3][kContactOwners];
+    int first[Owners];   // first reference of the owner's run
+    int fine[Owners];    // the run is a candidate-grid list (else a broadphase cell's)
+    int bcell[Owners];   // the owner's broadphase cell, x | y << 6 | z << 12
+    int satOn[Owners];   // owner takes part in the car-arena search (not demoed)
+    float rot[4][Owners];
     // screening, per owner: (cen, rayLo.x) (ax, rayLo.y) (ay, rayLo.z)
     // (az, rayHi.x) (rayHi.y, rayHi.z, screened, satOn); ax..az are the car's
     // box axes, ray* the box of the four ray segments
-    float4 scr[5][kContactOwners];
-    float nearPos[kMaxManifold][3][kContactOwners];
-    int nearN[kContactOwners];
-    int satHits[kContactOwners];
-    unsigned long long rayKey[kWheels][kContactOwners];
-    unsigned long long bestKey[kContactOwners];
-    float rayNrm[kWheels][3][kContactOwners];   // surface normal of each wheel's nearest arena hit
-    float bestPt[10][kContactOwners];           // manifold point of the deepest arena contact so far
+    float4 scr[5][Owners];
+    float nearPos[kMaxManifold][3][Owners];
+    int nearN[Owners];
+    int satHits[Owners];
+    unsigned long long rayKey[kWheels][Owners];
+    unsigned long long bestKey[Owners];
+    float rayNrm[kWheels][3][Owners];   // surface normal of each wheel's nearest arena hit
+    float bestPt[10][Owners];           // manifold point of the deepest arena contact so far
     // screened items in run order, entries owner << 24 | item
     int candQ[128];
     int candN;
 };
+using ContactLds = ContactLdsT<kContactOwners>;
 
 constexpr unsigned long long kNoKey = ~0ull;
 
-DI V3 ownerCen(const ContactLds& L, int o)
+template <int Owners>
+DI V3 ownerCen(const ContactLdsT<Owners>& L, int o)
 {
     const float4 c = L.scr[0][o];
     return V3{ c.x, c.y, c.z };
 }
 // suspension ray direction: minus the car's up axis
-DI V3 ownerDir(const ContactLds& L, int o)
+template <int Owners>
+DI V3 ownerDir(const ContactLdsT<Owners>& L, int o)
 {
     const float4 a = L.scr[3][o];
     return V3{ -a.x, -a.y, -a.z };
@@ -1021,7 +1025,8 @@ DI bool registeredIn(uint32_t reg, int bcell)
 // item).  An item of a candidate-grid run counts only when the triangle is
 // listed in the owner's broadphase cell: the reference tests exactly the
 // triangles of that cell.
-DI RefBox contactFetch(const Dev& d, const ContactLds& L, int o, int q, bool valid)
+template <int Owners>
+DI RefBox contactFetch(const Dev& d, const ContactLdsT<Owners>& L, int o, int q, bool valid)
 {
     const int ref = valid ? L.first[o] + q : 0;
     const bool fine = L.fine[o] != 0;
@@ -1046,7 +1051,8 @@ DI bool boxAxisMiss(V3 axis, V3 w, V3 half, float face)
 }
 
 // screen stage: queue the item unless the heavy stage provably rejects it
-DI void contactScreen(ContactLds& L, const RefBox& b, int o, int q, int lane)
+template <int Owners>
+DI void contactScreen(ContactLdsT<Owners>& L, const RefBox& b, int o, int q, int lane)
 {
     const float4 s0 = L.scr[0][o], s1 = L.scr[1][o], s2 = L.scr[2][o], s3 = L.scr[3][o], s4 = L.scr[4][o];
     const V3 tlo{ b.lo.x, b.lo.y, b.lo.z }, thi{ b.hi.x, b.hi.y, b.hi.z };
@@ -1084,7 +1090,8 @@ DI void contactScreen(ContactLds& L, const RefBox& b, int o, int q, int lane)
 // consecutive lanes.  SAT hits within the owner's first kMaxTriHits generate
 // their contacts here; each wheel's nearest ray hit so far leaves its normal
 // in LDS, so the owner needs no triangle load afterwards.
-DI void contactHeavy(const Dev& d, ContactLds& L, int lane)
+template <int Owners>
+DI void contactHeavy(const Dev& d, ContactLdsT<Owners>& L, int lane)
 {
     const int n = L.candN;
     const int take = n < 64 ? n : 64;
@@ -1104,9 +1111,12 @@ DI void contactHeavy(const Dev& d, ContactLds& L, int lane)
         const float det = dot(t.e1, pv);
         if (!(fabsf(det) < 1e-8f)) {
             const float invDet = 1.f / det;
+            // the owner's ray starts, computed as contactPrepare computed them
+            const Q4 orot{ L.rot[0][o], L.rot[1][o], L.rot[2][o], L.rot[3][o] };
+            const V3 ocen = ownerCen(L, o);
 #pragma unroll
             for (int k = 0; k < kWheels; k++) {
-                const V3 st{ L.start[k][0][o], L.start[k][1][o], L.start[k][2][o] };
+                const V3 st = wheelStart(ocen, orot, k);
                 const V3 tv = st - t.v0;
                 const float u = invDet * dot(tv, pv);
                 if (u < 0.f || u > 1.f) continue;
@@ -1193,7 +1203,8 @@ DI void contactHeavy(const Dev& d, ContactLds& L, int lane)
 }
 
 // after each screen round: drain full chunks; after the last, drain everything
-DI void contactDrain(const Dev& d, ContactLds& L, int lane, bool last)
+template <int Owners>
+DI void contactDrain(const Dev& d, ContactLdsT<Owners>& L, int lane, bool last)
 {
     waveSync();
     while (L.candN >= 64 || (last && L.candN > 0)) contactHeavy(d, L, lane);
@@ -1201,11 +1212,12 @@ DI void contactDrain(const Dev& d, ContactLds& L, int lane, bool last)
 
 // Owner side, before the search: pose, rays and (with sat) the plane points
 // of the car-arena search into LDS.  Lanes past the owners only reset the queue.
-DI void contactPrepare(ContactLds& L, int lane, bool sat, V3 cen, Q4 rot, int first, bool fine, int bcell,
+template <int Owners>
+DI void contactPrepare(ContactLdsT<Owners>& L, int lane, bool sat, V3 cen, Q4 rot, int first, bool fine, int bcell,
                        bool screen)
 {
     if (lane == 0) L.candN = 0;
-    if (lane >= kContactOwners) return;
+    if (lane >= Owners) return;
     const V3 dir = -rotate(rot, kZ);
     L.first[lane] = first;
     L.fine[lane] = fine;
@@ -1220,7 +1232,6 @@ DI void contactPrepare(ContactLds& L, int lane, bool sat, V3 cen, Q4 rot, int fi
         const V3 en = st + dir * (wheelRay(k) + 1.f);
         lo = vmin(lo, vmin(st, en));
         hi = vmax(hi, vmax(st, en));
-        L.start[k][0][lane] = st.x; L.start[k][1][lane] = st.y; L.start[k][2][lane] = st.z;
         L.rayKey[k][lane] = kNoKey;
     }
     const bool screened = screen && fabsf(cen.x) < kScreenRange && fabsf(cen.y) < kScreenRange &&
@@ -1245,7 +1256,8 @@ DI void contactPrepare(ContactLds& L, int lane, bool sat, V3 cen, Q4 rot, int fi
 
 // Owner side, after the search: wheel hits (arena winner, then cars and the
 // ball) and the cell reference of the deepest arena contact (-1 for none).
-DI int contactFinish(const Dev& d, const ContactLds& L, int lane, int car, int sim, V3 cen, Q4 rot, Wheels& w)
+template <int Owners>
+DI int contactFinish(const Dev& d, const ContactLdsT<Owners>& L, int lane, int car, int sim, V3 cen, Q4 rot, Wheels& w)
 {
     const V3 up = rotate(rot, kZ);
     const V3 dir = -up;

@@ -110,14 +110,15 @@ static_assert(sq(kHalf.x) + sq(kHalf.y) + sq(kHalf.z) < sq(kGridReach), "car box
 static_assert(sq(kFrontX) + sq(kFrontY) + sq(kFrontRay + 1.f) < sq(kGridReach), "front rays beyond the grid");
 static_assert(sq(kBackX) + sq(kBackY) + sq(kBackRay + 1.f) < sq(kGridReach), "back rays beyond the grid");
 
-// The contact search of cars [car0, car0 + kContactOwners) (those below
+// The contact search of cars [car0, car0 + Owners) (those below
 // carEnd) by one wave; L is that wave's own LDS.  Every lane of the wave calls
 // it; it synchronises the wave only.
-template <int Depth>
-DI void contactGroup(const Dev& d, uint32_t* __restrict__ ws, int screen, int car0, int carEnd, ContactLds& L, int lane)
+template <int Depth, int Owners>
+DI void contactGroup(const Dev& d, uint32_t* __restrict__ ws, int screen, int car0, int carEnd,
+                     ContactLdsT<Owners>& L, int lane)
 {
     const int car = car0 + lane;
-    const bool ok = lane < kContactOwners && car < carEnd;
+    const bool ok = lane < Owners && car < carEnd;
     V3 cen = kZero;
     Q4 rot{ 0.f, 0.f, 0.f, 1.f };
     Broad bp{ 0, 0, 0 };
@@ -166,7 +167,7 @@ DI void contactGroup(const Dev& d, uint32_t* __restrict__ ws, int screen, int ca
 __global__ __launch_bounds__(kContactBlock) void contactKernel(Dev d, uint32_t* __restrict__ ws, int screen, SimRange range)
 {
     __shared__ ContactLds L;
-    contactGroup<1>(d, ws, screen, range.begin * d.nCars + blockIdx.x * kContactOwners, range.end * d.nCars, L,
+    contactGroup<1, kContactOwners>(d, ws, screen, range.begin * d.nCars + blockIdx.x * kContactOwners, range.end * d.nCars, L,
                     threadIdx.x);
 }
 
@@ -351,16 +352,25 @@ constexpr int kDefaultWindowSims = CARL_WINDOW_SIMS;
 #define CARL_WINDOW_CONTACT_DEPTH 1
 #endif
 constexpr int kWindowContactDepth = CARL_WINDOW_CONTACT_DEPTH;
+// cars whose contacts one wave of the window kernel searches together
+#ifndef CARL_WINDOW_CONTACT_OWNERS
+#define CARL_WINDOW_CONTACT_OWNERS 64
+#endif
+constexpr int kWindowContactOwners = CARL_WINDOW_CONTACT_OWNERS;
 
-// Each wave's contact-search and ball-gather areas have LDS of their own
-// (35.4 KB per workgroup; four workgroups per CU, the occupancy the 256-VGPR
-// budget allows, use 141 KB of the 160 KB), so no wave can overwrite another
-// wave's area whatever the phase order.  The phases are still separated by
-// workgroup barriers: a phase reads state words other threads of the
-// workgroup wrote in the phase before.
+// Each wave has an LDS area of its own, used by its contact search and, in
+// the ball phase, by its ball gather (the two phases of one wave never
+// overlap, and no wave touches another wave's area).  With a whole wave of
+// contact owners that is 19.7 KB per wave, 39.4 KB per workgroup: four
+// workgroups per CU, the occupancy the 256-VGPR budget allows.  The phases are
+// still separated by workgroup barriers: a phase reads state words other
+// threads of the workgroup wrote in the phase before.
+union WaveLds {
+    ContactLdsT<kWindowContactOwners> contact;
+    BallLds ball;
+};
 struct WindowLds {
-    ContactLds contact[kWindowWaves];
-    BallLds ball[kWindowWaves];
+    WaveLds wave[kWindowWaves];
 };
 static_assert(4 * sizeof(WindowLds) <= 160 * 1024, "four window workgroups per CU");
 
@@ -413,15 +423,16 @@ DI void tickWindowBody(Dev d, uint32_t* __restrict__ ws, int screen, int kind, c
     }
     for (int k = 0; k < ticks; k++) {
         const int tick = tick0 + k;
-        for (int g = car0 + wave * kContactOwners; g < carEnd; g += kWindowWaves * kContactOwners)
-            contactGroup<kWindowContactDepth>(d, ws, screen, g, carEnd, L.contact[wave], lane);
+        for (int g = car0 + wave * kWindowContactOwners; g < carEnd; g += kWindowWaves * kWindowContactOwners)
+            contactGroup<kWindowContactDepth, kWindowContactOwners>(d, ws, screen, g, carEnd, L.wave[wave].contact,
+                                                                     lane);
         __syncthreads();
         mark(kStageContact);
         for (int c = car0 + t; c < carEnd; c += kWindowBlock) carArenaCar(d, ws, kind, actions, tick, c);
         __syncthreads();
         mark(kStageCarArena);
         for (int g = sim0 + wave * kBallOwners; g < simEnd; g += kWindowWaves * kBallOwners)
-            ballGroup<Native>(d, tick, g, simEnd, L.ball[wave], lane);
+            ballGroup<Native>(d, tick, g, simEnd, L.wave[wave].ball, lane);
         __syncthreads();
         mark(kStageBall);
         for (int c = car0 + t; c < carEnd; c += kWindowBlock) finishCar(d, c);
