@@ -1374,7 +1374,10 @@ DI void finishBall(const Dev& d, int s)
 
 // pads of one simulation, in pad order; the last overlapping car takes the pad.
 // The cars' positions, demo flags and boost live in registers for the whole
-// pass (at most kMaxCars per simulation); boosts are written back once.
+// pass (at most MaxCars per simulation, the loops over them unrolled);
+// boosts are written back once.  The pass is instantiated for two, four and
+// eight cars, so that 1v1 runs a quarter of the 8-car code (measured 3% per
+// step on the 1v1 window kernel).
 constexpr int kMaxCars = 8;
 
 // Boost pads [p0, p1) of simulation s: cooldowns, pickups and the boost
@@ -1384,14 +1387,15 @@ constexpr int kMaxCars = 8;
 // in any order, with the same result.  A thread reads every car's boost but
 // uses it only for a car inside one of its own pads, the only case in which
 // it writes that boost.
-DI void boostPadsRange(const Dev& d, int s, int p0, int p1)
+template <int MaxCars>
+DI void boostPadsRangeT(const Dev& d, int s, int p0, int p1)
 {
     const int base = s * d.nCars;
-    V3 cp[kMaxCars];
-    bool alive[kMaxCars];
-    float boost[kMaxCars];
+    V3 cp[MaxCars];
+    bool alive[MaxCars];
+    float boost[MaxCars];
 #pragma unroll
-    for (int k = 0; k < kMaxCars; k++) {
+    for (int k = 0; k < MaxCars; k++) {
         alive[k] = false;
         cp[k] = kZero;
         boost[k] = 0.f;
@@ -1419,7 +1423,7 @@ DI void boostPadsRange(const Dev& d, int s, int p0, int p1)
             int locked = -1;
             float have = 0.f;
 #pragma unroll
-            for (int k = 0; k < kMaxCars; k++) {
+            for (int k = 0; k < MaxCars; k++) {
                 if (k >= d.nCars || !alive[k]) continue;
                 const float dx = cp[k].x - px, dy = cp[k].y - py;
                 if (dx * dx + dy * dy < radius * radius && fabsf(cp[k].z - pz) < kPadHeight) {
@@ -1437,8 +1441,15 @@ DI void boostPadsRange(const Dev& d, int s, int p0, int p1)
         if (__float_as_uint(cd) != __float_as_uint(prev)) d.ssetf(CARL_SIM_PAD_COOLDOWN + p, s, cd);
     }
 #pragma unroll
-    for (int k = 0; k < kMaxCars; k++)
+    for (int k = 0; k < MaxCars; k++)
         if (changed & (1 << k)) d.setf(CARL_CAR_BOOST, base + k, boost[k]);
+}
+
+DI void boostPadsRange(const Dev& d, int s, int p0, int p1)
+{
+    if (d.nCars <= 2) boostPadsRangeT<2>(d, s, p0, p1);
+    else if (d.nCars <= 4) boostPadsRangeT<4>(d, s, p0, p1);
+    else boostPadsRangeT<kMaxCars>(d, s, p0, p1);
 }
 
 DI void boostPads(const Dev& d, int s) { boostPadsRange(d, s, 0, kPads); }
