@@ -84,6 +84,25 @@ DI void wsPut(uint32_t* ws, int n, int plane, int car, uint32_t v)
     __builtin_amdgcn_raw_buffer_store_b32(v, wsRsrc(ws, n), Dev::itemOff(car, kWsPlanes), plane * 256, 0);
 }
 
+// Where the contact phase leaves each car's wheel hits and deepest contact
+// (kWsPlanes words) for the car-arena phase.  Between the phase kernels: the
+// tick workspace in HBM.
+struct WsHandoff {
+    uint32_t* ws;
+    int n;
+    DI uint32_t get(int plane, int car, int) const { return wsGet(ws, n, plane, car); }
+    DI void put(int plane, int car, int, uint32_t v) const { wsPut(ws, n, plane, car, v); }
+};
+
+// In the window kernel: the LDS of the wave that searched the car, since the
+// lane that searches a car's contacts is the lane that runs its car-arena
+// step (words kWsPlanes x 64, indexed by lane).
+struct LdsHandoff {
+    uint32_t* slots;
+    DI uint32_t get(int plane, int, int lane) const { return slots[plane * 64 + lane]; }
+    DI void put(int plane, int, int lane, uint32_t v) const { slots[plane * 64 + lane] = v; }
+};
+
 // Simulations [begin, end) of one launch: the tick runs as independent
 // partitions on separate streams so the tail of one partition's kernel
 // overlaps the next kernel of the other.
@@ -113,9 +132,9 @@ static_assert(sq(kBackX) + sq(kBackY) + sq(kBackRay + 1.f) < sq(kGridReach), "ba
 // The contact search of cars [car0, car0 + Owners) (those below
 // carEnd) by one wave; L is that wave's own LDS.  Every lane of the wave calls
 // it; it synchronises the wave only.
-template <int Depth, int Owners>
-DI void contactGroup(const Dev& d, uint32_t* __restrict__ ws, int screen, int car0, int carEnd,
-                     ContactLdsT<Owners>& L, int lane)
+template <int Depth, int Owners, class Handoff>
+DI void contactGroup(const Dev& d, const Handoff& out, int screen, int car0, int carEnd, ContactLdsT<Owners>& L,
+                     int lane)
 {
     const int car = car0 + lane;
     const bool ok = lane < Owners && car < carEnd;
@@ -145,52 +164,62 @@ DI void contactGroup(const Dev& d, uint32_t* __restrict__ ws, int screen, int ca
         [&](const RefBox& b, int o, int q, int) { contactScreen(L, b, o, q, lane); },
         [&](bool last) { contactDrain(d, L, lane, last); });
     waveSync();
-    if (!ok) return;
     Wheels w;
-    const int best = contactFinish(d, L, lane, car, car / d.nCars, cen, rot, w);
-    const int n = d.nTotal;
+    int best = -1;
+    float pt[10] = {};
+    if (ok) {
+        best = contactFinish(d, L, lane, car, car / d.nCars, cen, rot, w);
+        if (best >= 0) {
+#pragma unroll
+            for (int i = 0; i < 10; i++) pt[i] = L.bestPt[i][lane];
+        }
+    }
+    // every lane's reads of the search area come before any lane's handoff
+    // writes (an LDS handoff may share that area)
+    waveSync();
+    if (!ok) return;
 #pragma unroll
     for (int k = 0; k < kWheels; k++) {
-        wsPut(ws, n, kWsDist + k, car, __float_as_uint(w.dist[k]));
-        wsPut(ws, n, kWsNx + k, car, __float_as_uint(w.normal[k].x));
-        wsPut(ws, n, kWsNy + k, car, __float_as_uint(w.normal[k].y));
-        wsPut(ws, n, kWsNz + k, car, __float_as_uint(w.normal[k].z));
-        wsPut(ws, n, kWsSrc + k, car, (uint32_t)w.src[k]);
+        out.put(kWsDist + k, car, lane, __float_as_uint(w.dist[k]));
+        out.put(kWsNx + k, car, lane, __float_as_uint(w.normal[k].x));
+        out.put(kWsNy + k, car, lane, __float_as_uint(w.normal[k].y));
+        out.put(kWsNz + k, car, lane, __float_as_uint(w.normal[k].z));
+        out.put(kWsSrc + k, car, lane, (uint32_t)w.src[k]);
     }
-    wsPut(ws, n, kWsBest, car, (uint32_t)best);
+    out.put(kWsBest, car, lane, (uint32_t)best);
     if (best >= 0) {
 #pragma unroll
-        for (int i = 0; i < 10; i++) wsPut(ws, n, kWsMan + i, car, __float_as_uint(L.bestPt[i][lane]));
+        for (int i = 0; i < 10; i++) out.put(kWsMan + i, car, lane, __float_as_uint(pt[i]));
     }
 }
 
 __global__ __launch_bounds__(kContactBlock) void contactKernel(Dev d, uint32_t* __restrict__ ws, int screen, SimRange range)
 {
     __shared__ ContactLds L;
-    contactGroup<1, kContactOwners>(d, ws, screen, range.begin * d.nCars + blockIdx.x * kContactOwners, range.end * d.nCars, L,
+    contactGroup<1, kContactOwners>(d, WsHandoff{ ws, d.nTotal }, screen, range.begin * d.nCars + blockIdx.x * kContactOwners, range.end * d.nCars, L,
                     threadIdx.x);
 }
 
 // A2: controls, car-arena contacts, suspension and the contact solve.
 // two waves per SIMD keep all of its waves resident at 65536 1v1 simulations
-DI void carArenaCar(const Dev& d, const uint32_t* __restrict__ ws, int kind, const void* __restrict__ actions,
-                    int tick, int car)
+template <class Handoff>
+DI void carArenaCar(const Dev& d, const Handoff& in, int kind, const void* __restrict__ actions, int tick, int car,
+                    int lane)
 {
-    const int n = d.nTotal;
     Wheels w;
 #pragma unroll
     for (int k = 0; k < kWheels; k++) {
-        w.dist[k] = __uint_as_float(wsGet(ws, n, kWsDist + k, car));
-        w.normal[k] = V3{ __uint_as_float(wsGet(ws, n, kWsNx + k, car)), __uint_as_float(wsGet(ws, n, kWsNy + k, car)),
-                          __uint_as_float(wsGet(ws, n, kWsNz + k, car)) };
-        w.src[k] = (int)wsGet(ws, n, kWsSrc + k, car);
+        w.dist[k] = __uint_as_float(in.get(kWsDist + k, car, lane));
+        w.normal[k] = V3{ __uint_as_float(in.get(kWsNx + k, car, lane)), __uint_as_float(in.get(kWsNy + k, car, lane)),
+                          __uint_as_float(in.get(kWsNz + k, car, lane)) };
+        w.src[k] = (int)in.get(kWsSrc + k, car, lane);
     }
-    const int best = (int)wsGet(ws, n, kWsBest, car);
+    const int best = (int)in.get(kWsBest, car, lane);
     ManPt bestPt{};
     if (best >= 0) {
         float v[10];
 #pragma unroll
-        for (int i = 0; i < 10; i++) v[i] = __uint_as_float(wsGet(ws, n, kWsMan + i, car));
+        for (int i = 0; i < 10; i++) v[i] = __uint_as_float(in.get(kWsMan + i, car, lane));
         bestPt = ManPt{ V3{ v[0], v[1], v[2] }, V3{ v[3], v[4], v[5] }, V3{ v[6], v[7], v[8] }, v[9] };
     }
     const Controls ctl = decodeControls(kind, actions, car);
@@ -216,7 +245,8 @@ __global__ __launch_bounds__(kTickBlock, 2) void carArenaKernel(Dev d, const uin
                                                              SimRange range)
 {
     const int car = range.begin * d.nCars + blockIdx.x * kTickBlock + threadIdx.x;
-    if (car < range.end * d.nCars) carArenaCar(d, ws, kind, actions, tick, car);
+    if (car < range.end * d.nCars)
+        carArenaCar(d, WsHandoff{ const_cast<uint32_t*>(ws), d.nTotal }, kind, actions, tick, car, (int)threadIdx.x & 63);
 }
 
 // Episode clock and the car-car pairs of one simulation, (b, a) with b the
@@ -358,17 +388,23 @@ constexpr int kWindowContactDepth = CARL_WINDOW_CONTACT_DEPTH;
 #endif
 constexpr int kWindowContactOwners = CARL_WINDOW_CONTACT_OWNERS;
 
-// Each wave has an LDS area of its own, used by its contact search and, in
-// the ball phase, by its ball gather (the two phases of one wave never
-// overlap, and no wave touches another wave's area).  With a whole wave of
+// Each wave has an LDS area of its own, used by its contact search, then by
+// the contact results it hands to the car-arena phase, and in the ball phase
+// by its ball gather (the phases of one wave never overlap, and no wave
+// touches another wave's area).  With a whole wave of
 // contact owners that is 19.7 KB per wave, 39.4 KB per workgroup: four
 // workgroups per CU, the occupancy the 256-VGPR budget allows.  The phases are
 // still separated by workgroup barriers: a phase reads state words other
 // threads of the workgroup wrote in the phase before.
 union WaveLds {
     ContactLdsT<kWindowContactOwners> contact;
+    uint32_t hand[kWsPlanes * 64];   // the contact phase's results, read by the car-arena phase
     BallLds ball;
 };
+// Car car0 + 64 w + l is contact owner l of wave w and car-arena thread
+// 64 w + l: a block holds at most kWindowBlock cars, one contact group per
+// wave, so each car's handoff stays in the lane that produced it.
+static_assert(kWindowContactOwners == 64, "the LDS handoff pairs contact owners with car-arena threads");
 struct WindowLds {
     WaveLds wave[kWindowWaves];
 };
@@ -427,11 +463,12 @@ DI void tickWindowBody(Dev d0, uint32_t* __restrict__ ws, int screen, int kind, 
     for (int k = 0; k < ticks; k++) {
         const int tick = tick0 + k;
         for (int g = car0 + wave * kWindowContactOwners; g < carEnd; g += kWindowWaves * kWindowContactOwners)
-            contactGroup<kWindowContactDepth, kWindowContactOwners>(d, ws, screen, g, carEnd, L.wave[wave].contact,
-                                                                     lane);
+            contactGroup<kWindowContactDepth, kWindowContactOwners>(d, LdsHandoff{ L.wave[wave].hand }, screen, g,
+                                                                     carEnd, L.wave[wave].contact, lane);
         __syncthreads();
         mark(kStageContact);
-        for (int c = car0 + t; c < carEnd; c += kWindowBlock) carArenaCar(d, ws, kind, actions, tick, c);
+        for (int c = car0 + t; c < carEnd; c += kWindowBlock)
+            carArenaCar(d, LdsHandoff{ L.wave[wave].hand }, kind, actions, tick, c, lane);
         __syncthreads();
         mark(kStageCarArena);
         for (int g = sim0 + wave * kBallOwners; g < simEnd; g += kWindowWaves * kBallOwners)
