@@ -211,20 +211,20 @@ def test_per_tick_from_identical_state(gpu):
     p.close()
 
 
-def test_long_run_error_growth_1v1(gpu):
-    """1,000 ticks without resynchronisation: report and bound the state error."""
+def test_thousand_ticks_stay_bit_exact_1v1(gpu):
+    """1,000 ticks (125 steps of 8) without resynchronisation: every state
+    field and every output stays bit-equal to the oracle after every step.
+    The trajectories are chaotic - a one-ulp change to one car's starting
+    velocity ends tens of uu away after these 1,000 ticks
+    (test_oracle_invariants.py::test_one_ulp_grows_past_the_long_run_tolerance)
+    - so a tolerance of 1e-3 uu over 1,000 ticks could only be met bit for
+    bit, and a single differing rounding in the engine would show here."""
     rng = np.random.default_rng(10)
     n = 32
     p = Pair(n, 1, 1, seed=17, frameskip=8)
     p.apply_reset_state(workloads.random_reset_state(rng, n, 2))
-    worst = 0.0
     for step in range(125):
         p.step_continuous(workloads.random_continuous_actions(rng, n, 2))
-        gc, _, _ = gpu_state(p.gpu)
-        oc, _, _ = p.cpu.export_state()
-        pos_g = gc[0:3].view(np.float32)
-        pos_o = oc[0:3].view(np.float32)
-        worst = max(worst, float(np.abs(pos_g.astype(np.float64) - pos_o).max()))
-    print(f"max car position error over 1000 ticks: {worst:.3g} uu")
-    assert worst <= 1e-3
+        report = p.state_mismatches() + p.output_mismatches()
+        assert not report, f"after step {step}:\n  " + "\n  ".join(report)
     p.close()

@@ -362,3 +362,35 @@ def test_suspension_rays_match_brute_force_over_the_mesh(arena):
                 assert source[i, k] == 0, (i, k, t)
     assert hits > 150
     env.close()
+
+
+def test_one_ulp_grows_past_the_long_run_tolerance():
+    """The trajectories are chaotic: 32 1v1 simulations from random states,
+    run twice for 1,000 ticks on the same actions, the second time with one
+    car's starting x velocity moved by one ulp, end more than 1 uu apart -
+    past a tolerance of 1e-3 uu over 1,000 ticks by three orders of
+    magnitude.  A comparison of the engine with the oracle at that tolerance
+    could only pass bit for bit, which is the bar the GPU parity tests hold."""
+    from carl_amd import workloads
+
+    rng = np.random.default_rng(10)
+    n = 32
+    reset = workloads.random_reset_state(rng, n, 2)
+    actions = [workloads.random_continuous_actions(rng, n, 2) for _ in range(125)]
+
+    def run(perturb):
+        env = OracleEnv(n, 1, 1, 17, 8)
+        state = {k: v.copy() for k, v in reset.items()}
+        if perturb:
+            v = state["car_velocity"]
+            v[:, 0, 0] = np.nextafter(v[:, 0, 0], np.float32(np.inf))
+        env.apply_reset_state(**state)
+        for a in actions:
+            env.step(a)
+        pos = env.export_state()[0][CAR_NAMES.index("CARL_CAR_POS_0"):][:3].view(np.float32).copy()
+        env.close()
+        return pos
+
+    drift = np.abs(run(False).astype(np.float64) - run(True)).max()
+    assert drift > 1.0, drift
+
