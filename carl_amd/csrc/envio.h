@@ -63,12 +63,17 @@ DI void packObservationPart(const Dev& d, int sim, int obs, bool invertOrange, b
     const V3 egoPos = d.cv(CARL_CAR_POS, ego);
     const int padCol = obsPadColumn(nC);
     if (part > 0) {
+        // An orange observer's slot p shows pad mirroredPad(p), which sits at
+        // pad p's position with x and y negated (the table is symmetric
+        // through the field centre): the position comes from the compile-time
+        // index p, not from a per-lane table lookup.
+        const float sgn = inv ? -1.f : 1.f;
 #pragma unroll
         for (int p = 0; p < kPads; p++) {
             if (p % 3 != part - 1) continue;
             const int pi = inv ? mirroredPad(p) : p;
             o[padCol + p] = d.sf(CARL_SIM_PAD_COOLDOWN + pi, sim) <= 0.f;
-            const float dist = len(egoPos - V3{ kPadPos[pi][0], kPadPos[pi][1], kPadPos[pi][2] });
+            const float dist = len(egoPos - V3{ kPadPos[p][0] * sgn, kPadPos[p][1] * sgn, kPadPos[p][2] });
             o[padCol + kPads + p] = normalizeObs ? dist / 14692.54f : dist;
         }
         return;

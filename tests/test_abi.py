@@ -87,3 +87,25 @@ def test_boost_pad_cylinders_are_disjoint():
     assert min(gaps) > 0.0, min(gaps)
     # the big pads are the six at |x| >= 3072 (corners and mid-field sides)
     assert all(abs(p[0]) >= 3072 for p in pads[:n_big])
+
+
+def test_boost_pad_table_is_point_symmetric():
+    """An orange observer sees pad slot p as pad mirroredPad(p); the packing
+    kernels take that pad's position as pad p's with x and y negated, which is
+    the same position only if the table is symmetric through the field centre
+    under the engine's mirror map."""
+    import re
+    from pathlib import Path
+
+    text = (Path(__file__).resolve().parents[1] / "carl_amd" / "csrc" / "constants.h").read_text()
+    body = text[text.index("kPadPos[kPads][3] = {"):]
+    body = body[:body.index("};")]
+    pads = [tuple(float(v) for v in m) for m in re.findall(r"\{\s*(-?[\d.]+)f,\s*(-?[\d.]+)f,\s*(-?[\d.]+)f\s*\}", body)]
+    fn = text[text.index("HDI int mirroredPad(int p)"):]
+    fn = fn[:fn.index("}\n") + 1]
+    # the map as written: p >= 6 -> 39 - p, p < 2 -> 1 - p, else 7 - p
+    assert "if (p >= 6) return 39 - p;" in fn and "return p < 2 ? 1 - p : 7 - p;" in fn
+    mirror = [39 - p if p >= 6 else (1 - p if p < 2 else 7 - p) for p in range(34)]
+    assert sorted(mirror) == list(range(34))
+    for p, q in enumerate(mirror):
+        assert pads[q] == (-pads[p][0], -pads[p][1], pads[p][2]), (p, q)
