@@ -68,11 +68,19 @@ DI void packObservationPart(const Dev& d, int sim, int obs, bool invertOrange, b
         // through the field centre): the position comes from the compile-time
         // index p, not from a per-lane table lookup.
         const float sgn = inv ? -1.f : 1.f;
+        // the part's pads p = part - 1, part + 2, ...: a loop over the part's
+        // own pads only, each pad's position a wave-uniform table entry
+        float cool[(kPads + 2) / 3];
 #pragma unroll
-        for (int p = 0; p < kPads; p++) {
-            if (p % 3 != part - 1) continue;
-            const int pi = inv ? mirroredPad(p) : p;
-            o[padCol + p] = d.sf(CARL_SIM_PAD_COOLDOWN + pi, sim) <= 0.f;
+        for (int i = 0; i < (kPads + 2) / 3; i++) {
+            const int p = part - 1 + 3 * i;
+            cool[i] = p < kPads ? d.sf(CARL_SIM_PAD_COOLDOWN + (inv ? mirroredPad(p) : p), sim) : 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < (kPads + 2) / 3; i++) {
+            const int p = part - 1 + 3 * i;
+            if (p >= kPads) break;
+            o[padCol + p] = cool[i] <= 0.f;
             const float dist = len(egoPos - V3{ kPadPos[p][0] * sgn, kPadPos[p][1] * sgn, kPadPos[p][2] });
             o[padCol + kPads + p] = normalizeObs ? dist / 14692.54f : dist;
         }
