@@ -1405,10 +1405,12 @@ DI void boostPadsRangeT(const Dev& d, int s, int p0, int p1)
             boost[k] = d.cf(CARL_CAR_BOOST, base + k);
         }
     }
-    // all cooldowns of the range are read before any is written back
+    // all cooldowns are read before any is written back, each load
+    // unconditional (one batch in flight; a load under a per-pad range test
+    // would wait for its own round trip), those outside the range unused
     float cool[kPads];
 #pragma unroll
-    for (int p = 0; p < kPads; p++) cool[p] = p >= p0 && p < p1 ? d.sf(CARL_SIM_PAD_COOLDOWN + p, s) : 0.f;
+    for (int p = 0; p < kPads; p++) cool[p] = d.sf(CARL_SIM_PAD_COOLDOWN + p, s);
     int changed = 0;
 #pragma unroll
     for (int p = 0; p < kPads; p++) {
