@@ -223,6 +223,9 @@ DI void carArenaCar(const Dev& d, const Handoff& in, int kind, const void* __res
         bestPt = ManPt{ V3{ v[0], v[1], v[2] }, V3{ v[3], v[4], v[5] }, V3{ v[6], v[7], v[8] }, v[9] };
     }
     const Controls ctl = decodeControls(kind, actions, car);
+    const bool demoed = d.ci(CARL_CAR_DEMOED, car) != 0;
+    CarRegs r;
+    loadRegs(d, car, r);
     storeWheelOutputs(d, car, w);
     d.setf(CARL_CAR_CTRL_THROTTLE, car, ctl.throttle);
     d.setf(CARL_CAR_CTRL_STEER, car, ctl.steer);
@@ -232,9 +235,7 @@ DI void carArenaCar(const Dev& d, const Handoff& in, int kind, const void* __res
     d.seti(CARL_CAR_CTRL_JUMP, car, ctl.jump);
     d.seti(CARL_CAR_CTRL_BOOST, car, ctl.boost);
     d.seti(CARL_CAR_CTRL_SLIDE, car, ctl.slide);
-    if (d.ci(CARL_CAR_DEMOED, car)) return;
-    CarRegs r;
-    loadRegs(d, car, r);
+    if (demoed) return;
     applyControls(r, ctl, w);
     solveCarArena(r, w, best >= 0, bestPt, tick);
     storeRegs(d, car, r);

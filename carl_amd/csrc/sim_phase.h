@@ -1320,6 +1320,11 @@ DI void respawnCar(const Dev& d, int c)
 // integrate, then apply the impulse cache / demo timer (Solve.cuh:316-327, FinishTick.cuh:100-141)
 DI void finishCar(const Dev& d, int c)
 {
+    V3 pos = d.cv(CARL_CAR_POS, c), cen;
+    Q4 rot = d.cq(CARL_CAR_ROT, c);
+    V3 vel = d.cv(CARL_CAR_VEL, c), ang = d.cv(CARL_CAR_ANG, c);
+    const V3 imp = d.cv(CARL_CAR_IMP, c);
+    const float cd = d.cf(CARL_CAR_CONTACT_COOLDOWN, c);
     if (d.ci(CARL_CAR_DEMOED, c)) {
         float timer = d.cf(CARL_CAR_DEMO_TIMER, c);
         if (timer <= kDemoRespawnTime) {
@@ -1338,12 +1343,8 @@ DI void finishCar(const Dev& d, int c)
         if (timer <= 0.f) respawnCar(d, c);
         return;
     }
-    V3 pos = d.cv(CARL_CAR_POS, c), cen;
-    Q4 rot = d.cq(CARL_CAR_ROT, c);
-    V3 vel = d.cv(CARL_CAR_VEL, c), ang = d.cv(CARL_CAR_ANG, c);
     integratePose(pos, cen, rot, vel, ang);
     clampCarVelocity(vel, ang);
-    const V3 imp = d.cv(CARL_CAR_IMP, c);
     if (lensq(imp) > 1e-12f) {
         vel = vel + imp;
         const float ss = lensq(vel);
@@ -1355,7 +1356,6 @@ DI void finishCar(const Dev& d, int c)
     d.setq(CARL_CAR_ROT, c, rot);
     d.setv(CARL_CAR_VEL, c, vel);
     d.setv(CARL_CAR_ANG, c, ang);
-    const float cd = d.cf(CARL_CAR_CONTACT_COOLDOWN, c);
     if (cd > 0.f) d.setf(CARL_CAR_CONTACT_COOLDOWN, c, fmax_(cd - kDt, 0.f));
 }
 
