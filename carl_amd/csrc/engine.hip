@@ -603,6 +603,43 @@ HDI int packChunkRows(int rowLen)
 }
 HDI size_t packLdsBytes(int rowLen) { return (size_t)packChunkRows(rowLen) * packStride(rowLen) * sizeof(float); }
 
+// Stores `rows` whole rows (rowLen floats each, row stride `stride` floats in
+// LDS from `lds`) to the contiguous run at dst; 16 bytes per lane and
+// instruction when dst is 16-byte aligned.  Called by every thread of the
+// workgroup.
+DI void storeRunFromLds(float* dst, int rowLen, int stride, int rows, const float* lds)
+{
+    const int t = threadIdx.x, total = rows * rowLen;
+    if (((size_t)dst & 15) == 0) {
+        const int step = 4 * kPackBlock, rs = step / rowLen, cs = step % rowLen;
+        int rr = 4 * t / rowLen, c = 4 * t % rowLen;
+        for (int e = 4 * t; e + 3 < total; e += step) {
+            float v[4];
+            int r2 = rr, c2 = c;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                v[k] = lds[r2 * stride + c2];
+                if (++c2 == rowLen) { c2 = 0; r2++; }
+            }
+            *reinterpret_cast<float4*>(dst + e) = make_float4(v[0], v[1], v[2], v[3]);
+            rr += rs;
+            c += cs;
+            if (c >= rowLen) { c -= rowLen; rr++; }
+        }
+        const int e = (total & ~3) + t;
+        if (e < total) dst[e] = lds[(e / rowLen) * stride + e % rowLen];
+        return;
+    }
+    const int rowStep = kPackBlock / rowLen, colStep = kPackBlock % rowLen;
+    int rr = t / rowLen, c = t % rowLen;
+    for (int e = t; e < total; e += kPackBlock) {
+        dst[e] = lds[rr * stride + c];
+        rr += rowStep;
+        c += colStep;
+        if (c >= rowLen) { c -= rowLen; rr++; }
+    }
+}
+
 // Rows [r0, r1) of out (rowLen floats each): a row r with keep(r) is built by
 // part(r, q, dst) for q = 0..kRowParts-1 and stored; other rows are left
 // untouched.  Every thread of the workgroup calls this (it holds barriers);
@@ -624,28 +661,11 @@ DI void packRowsParts(float* out, int rowLen, int r0, int r1, Keep&& keep, Part&
         if (mine) part(c0 + lane, q, packLds + lane * stride);
         __syncthreads();
         float* dst = out + (size_t)c0 * rowLen;
-        const int total = rows * rowLen;
-        if (kept == kRowParts * rows && ((size_t)dst & 15) == 0) {
-            // every row kept: the chunk is one contiguous run, stored 16 bytes
-            // per lane and instruction
-            const int step = 4 * kPackBlock, rs = step / rowLen, cs = step % rowLen;
-            int rr = 4 * t / rowLen, c = 4 * t % rowLen;
-            for (int e = 4 * t; e + 3 < total; e += step) {
-                float v[4];
-                int r2 = rr, c2 = c;
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    v[k] = packLds[r2 * stride + c2];
-                    if (++c2 == rowLen) { c2 = 0; r2++; }
-                }
-                *reinterpret_cast<float4*>(dst + e) = make_float4(v[0], v[1], v[2], v[3]);
-                rr += rs;
-                c += cs;
-                if (c >= rowLen) { c -= rowLen; rr++; }
-            }
-            const int e = (total & ~3) + t;
-            if (e < total) dst[e] = packLds[(e / rowLen) * stride + e % rowLen];
+        if (kept == kRowParts * rows) {
+            // every row kept: the chunk is one contiguous run
+            storeRunFromLds(dst, rowLen, stride, rows, packLds);
         } else {
+            const int total = rows * rowLen;
             int rr = t / rowLen, c = t % rowLen;
             for (int e = t; e < total; e += kPackBlock) {
                 if (on[rr]) dst[e] = packLds[rr * stride + c];
@@ -680,12 +700,18 @@ __global__ __launch_bounds__(kPackBlock) void obsKernel(Dev d, float* out, int o
 }
 
 // Everything an env step does after its ticks, for kStepSims simulations per
-// workgroup, in the reference's order: rewards and dones, the transition
-// state and the transition observations of finished simulations, their
-// resets, the match state, the observations and the state.  A simulation's
-// rows depend on nothing but its own state, so the workgroup needs only its
-// own barriers between the stages.
+// workgroup: rewards and dones, the transition state and the transition
+// observations of finished simulations, their resets, the match state, the
+// observations and the state, with the reference's data dependences (the
+// transition rows read the state before the resets, the others after).  A
+// simulation's rows depend on nothing but its own state, so the workgroup
+// needs only its own barriers.  Every wave decides the fate of the
+// workgroup's simulations (one per lane) from their match words, so the
+// finished ones are known to each wave without a barrier; the transition
+// observations of the first finished ones are built in the same round as
+// the transition state, in the LDS left over by the state rows.
 constexpr int kStepSims = 64;
+static_assert(kStepSims == 64, "one simulation per lane of each wave");
 
 struct StepIO {
     float *rewards, *tstate, *tobs, *obs, *state;
@@ -697,54 +723,102 @@ struct StepIO {
     DoneRule rule;
 };
 
+HDI size_t stepLdsBytes(int obsDim, int stateDim)
+{
+    const size_t a = packLdsBytes(obsDim), b = packLdsBytes(stateDim);
+    return a > b ? a : b;
+}
+
 __global__ __launch_bounds__(kPackBlock) void stepEnvKernel(Dev d, StepIO io)
 {
-    __shared__ int done[kStepSims];
-    __shared__ int fate[kStepSims];   // DoneOutcome of each simulation
-    const int t = threadIdx.x, nC = d.nCars;
+    extern __shared__ float packLds[];
+    const int t = threadIdx.x, lane = t & 63, q = t >> 6, nC = d.nCars;
     const int s0 = blockIdx.x * kStepSims, s1 = min(s0 + kStepSims, d.nSim);
-    const int s = s0 + t;
+    const int s = s0 + lane;
+    int outcome = kKept;
+    bool dn = false;
+    if (s < s1) {
+        const MatchWords m = matchWords(d, s);
+        dn = simDoneFrom(m, io.tickCount, io.rule);
+        outcome = doneOutcome(m, io.tickCount, io.rule);
+        if (q == 0) {
+            io.rewards[s] = (float)m.scorer;
+            io.dones[s] = dn;
+            io.tscore[s] = m.blue - m.orange;
+            io.tticks[s] = m.ep;
+            io.tovertime[s] = m.overtime != 0;
+            io.score[s] = outcome == kReset ? 0 : m.blue - m.orange;
+            io.ticks[s] = outcome == kReset ? 0 : m.ep;
+            io.overtime[s] = outcome == kReset ? false : (outcome == kOvertimeEntered || m.overtime != 0);
+        }
+    }
     if (io.actionCopy) {
         const size_t w0 = (size_t)s0 * nC * 7;
         for (int w = t; w < (s1 - s0) * nC * 7; w += kPackBlock) io.actionCopy[w0 + w] = io.actions[w0 + w];
     }
-    // rewards, dones and the transition match state; each simulation's
-    // reset outcome, and with it the match state after the resets, follows
-    // from the same words
-    if (s < s1) {
-        const MatchWords m = matchWords(d, s);
-        const bool dn = simDoneFrom(m, io.tickCount, io.rule);
-        const int outcome = doneOutcome(m, io.tickCount, io.rule);
-        io.rewards[s] = (float)m.scorer;
-        io.dones[s] = dn;
-        io.tscore[s] = m.blue - m.orange;
-        io.tticks[s] = m.ep;
-        io.tovertime[s] = m.overtime != 0;
-        io.score[s] = outcome == kReset ? 0 : m.blue - m.orange;
-        io.ticks[s] = outcome == kReset ? 0 : m.ep;
-        io.overtime[s] = outcome == kReset ? false : (outcome == kOvertimeEntered || m.overtime != 0);
-        done[t] = dn;
-        fate[t] = outcome;
+    // the finished simulations, the same mask in every wave; the transition
+    // observation rows of finished simulation j (in lane order) are
+    // doneRank(j) * nC .. + nC - 1
+    const uint64_t doneMask = __ballot(dn);
+    const int doneRows = __popcll(doneMask) * nC;
+    auto doneRank = [&](int local) { return __popcll(doneMask & ((1ull << local) - 1ull)); };
+
+    // round 1: the first chunk of transition state rows, and as many
+    // transition observation rows as fit beside them
+    const int sStride = packStride(io.stateDim), oStride = packStride(io.obsDim);
+    const int aRows = min(packChunkRows(io.stateDim), s1 - s0);
+    float* const ldsB = packLds + aRows * sStride;
+    const int capB = ((int)(stepLdsBytes(io.obsDim, io.stateDim) / sizeof(float)) - aRows * sStride) / oStride;
+    const int nB = min(doneRows, max(capB, 0));
+    if (lane < aRows) packStatePart(d, s0 + lane, io.frameskip, io.tickCount, q, packLds + lane * sStride);
+    if (lane < nB) {
+        // the lane-th finished row: its simulation is the (lane / nC)-th set bit of doneMask
+        uint64_t m = doneMask;
+        for (int k = 0; k < lane / nC; k++) m &= m - 1ull;
+        const int local = __ffsll((unsigned long long)m) - 1;
+        packObservationPart(d, s0 + local, lane % nC, io.invert != 0, io.normalize != 0, io.prev != 0, q,
+                            ldsB + lane * oStride);
     }
     __syncthreads();
-    packRowsParts(
-        io.tstate, io.stateDim, s0, s1, [](int) { return true; },
-        [&](int r, int q, float* o) { packStatePart(d, r, io.frameskip, io.tickCount, q, o); });
-    packRowsParts(
-        io.tobs, io.obsDim, s0 * nC, s1 * nC, [&](int a) { return done[a / nC - s0] != 0; },
-        [&](int a, int q, float* o) {
-            packObservationPart(d, a / nC, a % nC, io.invert != 0, io.normalize != 0, io.prev != 0, q, o);
-        });
-    if (s < s1) applyDoneOutcome(d, s, fate[t], io.tickCount, io.nOrange);
+    storeRunFromLds(io.tstate + (size_t)s0 * io.stateDim, io.stateDim, sStride, aRows, packLds);
+    {
+        // the listed rows, each a contiguous run of obsDim floats in tobs
+        const int total = nB * io.obsDim;
+        for (int e = t; e < total; e += kPackBlock) {
+            const int j = e / io.obsDim, c = e % io.obsDim;
+            uint64_t m = doneMask;
+            for (int k = 0; k < j / nC; k++) m &= m - 1ull;
+            const int row = (s0 + __ffsll((unsigned long long)m) - 1) * nC + j % nC;
+            io.tobs[(size_t)row * io.obsDim + c] = ldsB[j * oStride + c];
+        }
+    }
+    __syncthreads();
+    // the rest of the transition state (more cars than one chunk holds) and
+    // the transition observations that did not fit
+    if (s0 + aRows < s1)
+        packRowsParts(
+            io.tstate, io.stateDim, s0 + aRows, s1, [](int) { return true; },
+            [&](int r, int qq, float* o) { packStatePart(d, r, io.frameskip, io.tickCount, qq, o); });
+    if (doneRows > nB)
+        packRowsParts(
+            io.tobs, io.obsDim, s0 * nC, s1 * nC,
+            [&](int a) {
+                const int local = a / nC - s0;
+                return ((doneMask >> local) & 1ull) != 0 && doneRank(local) * nC + a % nC >= nB;
+            },
+            [&](int a, int qq, float* o) {
+                packObservationPart(d, a / nC, a % nC, io.invert != 0, io.normalize != 0, io.prev != 0, qq, o);
+            });
+    if (s < s1) applyDoneOutcomePart(d, s, outcome, io.tickCount, io.nOrange, q);
     __syncthreads();
     packRowsParts(
         io.obs, io.obsDim, s0 * nC, s1 * nC, [](int) { return true; },
-        [&](int a, int q, float* o) {
-            packObservationPart(d, a / nC, a % nC, io.invert != 0, io.normalize != 0, io.prev != 0, q, o);
+        [&](int a, int qq, float* o) {
+            packObservationPart(d, a / nC, a % nC, io.invert != 0, io.normalize != 0, io.prev != 0, qq, o);
         });
     packRowsParts(
         io.state, io.stateDim, s0, s1, [](int) { return true; },
-        [&](int r, int q, float* o) { packStatePart(d, r, 1, io.tickCount, q, o); });
+        [&](int r, int qq, float* o) { packStatePart(d, r, 1, io.tickCount, qq, o); });
 }
 
 __global__ void setBallKernel(Dev d, const float* pos, const float* vel, const float* ang, Selection sel)
@@ -1481,7 +1555,7 @@ int carl_env_step(carl_env* e, int kind, const void* actions)
     io.invert = e->invert; io.normalize = e->normalize; io.prev = e->prevControls;
     io.frameskip = e->frameskip; io.tickCount = e->tickCount; io.nOrange = e->nOrange;
     io.rule = e->rule();
-    const size_t lds = std::max(packLdsBytes(e->obsDim), packLdsBytes(e->stateDim));
+    const size_t lds = stepLdsBytes(e->obsDim, e->stateDim);
     CARL_TRY(launchTick(e, true, CARL_KERNEL_STEP_ENV, stepEnvKernel, dim3(e->grid(e->nSim, kStepSims)),
                         dim3(kPackBlock), (uint32_t)lds, e->stream, e->dev(), io));
     HIP_TRY(hipGetLastError());

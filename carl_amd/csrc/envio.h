@@ -48,6 +48,34 @@ constexpr int kRowParts = 4;
 // the kPads flags).
 HDI int obsPadColumn(int nCars) { return 9 + nCars * kObsPerCar; }
 
+// Pad columns of part Part > 0 of one observer's row: the flag and the
+// distance of the pads p = Part - 1, Part + 2, ... (p % 3 == Part - 1).  The
+// part is a template argument, so every pad index, its table position and its
+// mirrored index are compile-time constants: the positions fold into
+// immediates and no load waits on another.  An orange observer's slot p shows
+// pad mirroredPad(p), which sits at pad p's position with x and y negated
+// (the table is symmetric through the field centre); its cooldown field is
+// chosen per lane inside the load's offset.
+template <int Part>
+DI void packObservationPads(const Dev& d, int sim, bool inv, bool normalizeObs, V3 egoPos, int padCol, float* o)
+{
+    constexpr int kMine = (kPads - (Part - 1) + 2) / 3;
+    const float sgn = inv ? -1.f : 1.f;
+    float cool[kMine];
+#pragma unroll
+    for (int i = 0; i < kMine; i++) {
+        const int p = Part - 1 + 3 * i;
+        cool[i] = __uint_as_float(d.swLane(CARL_SIM_PAD_COOLDOWN + (inv ? mirroredPad(p) : p), sim));
+    }
+#pragma unroll
+    for (int i = 0; i < kMine; i++) {
+        const int p = Part - 1 + 3 * i;
+        o[padCol + p] = cool[i] <= 0.f;
+        const float dist = len(egoPos - V3{ kPadPos[p][0] * sgn, kPadPos[p][1] * sgn, kPadPos[p][2] });
+        o[padCol + kPads + p] = normalizeObs ? dist / 14692.54f : dist;
+    }
+}
+
 // Part `part` of one observer's row: ball, self, teammates, opponents, pads,
 // relative vectors, goals, dodge window, controller state [, previous
 // controls].  Part 0 writes every column except the pads' and normalises
@@ -62,29 +90,12 @@ DI void packObservationPart(const Dev& d, int sim, int obs, bool invertOrange, b
     const int ego = base + obs;
     const V3 egoPos = d.cv(CARL_CAR_POS, ego);
     const int padCol = obsPadColumn(nC);
-    if (part > 0) {
-        // An orange observer's slot p shows pad mirroredPad(p), which sits at
-        // pad p's position with x and y negated (the table is symmetric
-        // through the field centre): the position comes from the compile-time
-        // index p, not from a per-lane table lookup.
-        const float sgn = inv ? -1.f : 1.f;
-        // the part's pads p = part - 1, part + 2, ...: a loop over the part's
-        // own pads only, each pad's position a wave-uniform table entry
-        float cool[(kPads + 2) / 3];
-#pragma unroll
-        for (int i = 0; i < (kPads + 2) / 3; i++) {
-            const int p = part - 1 + 3 * i;
-            cool[i] = p < kPads ? d.sf(CARL_SIM_PAD_COOLDOWN + (inv ? mirroredPad(p) : p), sim) : 0.f;
-        }
-#pragma unroll
-        for (int i = 0; i < (kPads + 2) / 3; i++) {
-            const int p = part - 1 + 3 * i;
-            if (p >= kPads) break;
-            o[padCol + p] = cool[i] <= 0.f;
-            const float dist = len(egoPos - V3{ kPadPos[p][0] * sgn, kPadPos[p][1] * sgn, kPadPos[p][2] });
-            o[padCol + kPads + p] = normalizeObs ? dist / 14692.54f : dist;
-        }
-        return;
+    static_assert(kRowParts == 4, "three pad parts");
+    switch (part) {
+    case 1: packObservationPads<1>(d, sim, inv, normalizeObs, egoPos, padCol, o); return;
+    case 2: packObservationPads<2>(d, sim, inv, normalizeObs, egoPos, padCol, o); return;
+    case 3: packObservationPads<3>(d, sim, inv, normalizeObs, egoPos, padCol, o); return;
+    default: break;
     }
     const V3 ballPos = d.sv(CARL_SIM_BALL_POS, sim), ballVel = d.sv(CARL_SIM_BALL_VEL, sim);
     const V3 egoVel = d.cv(CARL_CAR_VEL, ego);
@@ -240,18 +251,34 @@ DI void kickoffCar(const Dev& d, int c, int loc, bool invert)
     resetInternal(d, c);
 }
 
-DI void kickoffSim(const Dev& d, int s, int tickCount, int nOrange)
+// The kickoff permutation of simulation s after a reset at tickCount.
+DI int kickoffPerm(const Dev& d, int s, int tickCount)
 {
     const uint32_t seed = mix32((uint32_t)d.seed) ^ mix32((uint32_t)s) ^ mix32((uint32_t)tickCount);
-    const int perm = pickIndex(seed, 120);
+    return pickIndex(seed, 120);
+}
+
+DI void kickoffBall(const Dev& d, int s)
+{
     d.ssetv(CARL_SIM_BALL_POS, s, V3{ 0.f, 0.f, kBallRestZ });
     d.ssetv(CARL_SIM_BALL_VEL, s, kZero);
     d.ssetv(CARL_SIM_BALL_ANG, s, kZero);
     d.sseti(CARL_SIM_BALL_INT_VALID, s, 0);
-    for (int team = 0; team < 2; team++) {
-        const int size = team ? nOrange : d.nBlue;
-        for (int i = 0; i < size; i++) kickoffCar(d, s * d.nCars + team * d.nBlue + i, kickoffSpawn(perm, i), team != 0);
-    }
+}
+
+// Car `local` of simulation s at its kickoff spawn (blue cars first, then
+// orange, each team numbered from 0 in the permutation).
+DI void kickoffLocalCar(const Dev& d, int s, int local, int perm)
+{
+    const bool orange = local >= d.nBlue;
+    kickoffCar(d, s * d.nCars + local, kickoffSpawn(perm, orange ? local - d.nBlue : local), orange);
+}
+
+DI void kickoffSim(const Dev& d, int s, int tickCount, int nOrange)
+{
+    const int perm = kickoffPerm(d, s, tickCount);
+    kickoffBall(d, s);
+    for (int k = 0; k < d.nBlue + nOrange; k++) kickoffLocalCar(d, s, k, perm);
 }
 
 DI void clearCarContacts(const Dev& d, int c)
@@ -311,6 +338,29 @@ DI int doneOutcome(const MatchWords& m, int tickCount, DoneRule rule)
     return kReset;
 }
 
+// The car words a done-reset writes for car `local` of simulation s.
+DI void resetCarAfterDone(const Dev& d, int s, int local, int perm)
+{
+    const int c = s * d.nCars + local;
+    kickoffLocalCar(d, s, local, perm);
+    d.seti(CARL_CAR_ARENA_CONTACT_TICK, c, -1);
+    clearCarContacts(d, c);
+    for (int w = 0; w < kWheels; w++) {
+        d.seti(CARL_CAR_WHEEL_SOURCE + w, c, kSrcNone);
+        d.seti(CARL_CAR_WHEEL_CONTACT + w, c, 0);
+    }
+}
+
+// The simulation words (match state, clock, ball) a done-reset writes.
+DI void resetSimWordsAfterDone(const Dev& d, int s, int tickCount)
+{
+    for (int f = CARL_SIM_BLUE_SCORE; f <= CARL_SIM_OVERTIME; f++) d.sseti(f, s, 0);
+    kickoffBall(d, s);
+    d.sseti(CARL_SIM_EPISODE_TICKS, s, 0);
+    d.sseti(CARL_SIM_LAST_TOUCH_TICK, s, tickCount);
+    d.sseti(CARL_SIM_BALL_ARENA_CONTACT_TICK, s, -1);
+}
+
 DI void applyDoneOutcome(const Dev& d, int s, int outcome, int tickCount, int nOrange)
 {
     if (outcome == kOvertimeEntered) {
@@ -318,21 +368,32 @@ DI void applyDoneOutcome(const Dev& d, int s, int outcome, int tickCount, int nO
         return;
     }
     if (outcome != kReset) return;
-    for (int f = CARL_SIM_BLUE_SCORE; f <= CARL_SIM_OVERTIME; f++) d.sseti(f, s, 0);
-    kickoffSim(d, s, tickCount, nOrange);
-    d.sseti(CARL_SIM_EPISODE_TICKS, s, 0);
-    d.sseti(CARL_SIM_LAST_TOUCH_TICK, s, tickCount);
-    d.sseti(CARL_SIM_BALL_ARENA_CONTACT_TICK, s, -1);
-    for (int k = 0; k < d.nCars; k++) {
-        const int c = s * d.nCars + k;
-        d.seti(CARL_CAR_ARENA_CONTACT_TICK, c, -1);
-        clearCarContacts(d, c);
-        for (int w = 0; w < kWheels; w++) {
-            d.seti(CARL_CAR_WHEEL_SOURCE + w, c, kSrcNone);
-            d.seti(CARL_CAR_WHEEL_CONTACT + w, c, 0);
-        }
-    }
+    const int perm = kickoffPerm(d, s, tickCount);
+    resetSimWordsAfterDone(d, s, tickCount);
+    for (int k = 0; k < d.nBlue + nOrange; k++) resetCarAfterDone(d, s, k, perm);
     for (int p = 0; p < kPads; p++) d.ssetf(CARL_SIM_PAD_COOLDOWN + p, s, 0.f);
+}
+
+// applyDoneOutcome shared by the kRowParts waves of a workgroup, each storing
+// its own fields: wave 0 the simulation words, wave 1 the pad cooldowns,
+// waves 2 and 3 the cars (car k by wave 2 + k % 2).  The waves write
+// disjoint words, so the result is the same as one wave's.
+DI void applyDoneOutcomePart(const Dev& d, int s, int outcome, int tickCount, int nOrange, int part)
+{
+    static_assert(kRowParts == 4, "four reset parts");
+    if (outcome == kOvertimeEntered) {
+        if (part == 0) d.sseti(CARL_SIM_OVERTIME, s, 1);
+        return;
+    }
+    if (outcome != kReset) return;
+    if (part == 0) {
+        resetSimWordsAfterDone(d, s, tickCount);
+    } else if (part == 1) {
+        for (int p = 0; p < kPads; p++) d.ssetf(CARL_SIM_PAD_COOLDOWN + p, s, 0.f);
+    } else {
+        const int perm = kickoffPerm(d, s, tickCount);
+        for (int k = part - 2; k < d.nBlue + nOrange; k += 2) resetCarAfterDone(d, s, k, perm);
+    }
 }
 
 DI void resetAfterDone(const Dev& d, int s, int tickCount, DoneRule rule, int nOrange)

@@ -123,6 +123,13 @@ struct Dev {
     DI void setv(int f, int i, V3 v) const { setf(f, i, v.x); setf(f + 1, i, v.y); setf(f + 2, i, v.z); }
     DI void setq(int f, int i, Q4 q) const { setf(f, i, q.x); setf(f + 1, i, q.y); setf(f + 2, i, q.z); setf(f + 3, i, q.w); }
 
+    // A field chosen per lane: the field part joins the per-item offset, so
+    // lanes with different fields still share one load instruction.
+    DI uint32_t swLane(int f, int s) const
+    {
+        return __builtin_amdgcn_raw_buffer_load_b32(simRsrc(), itemOff(s, CARL_SIM_FIELDS) + f * 256, 0, 0);
+    }
+
     DI float sf(int f, int s) const { return __uint_as_float(sw(f, s)); }
     DI int si(int f, int s) const { return (int)sw(f, s); }
     DI V3 sv(int f, int s) const { return V3{ sf(f, s), sf(f + 1, s), sf(f + 2, s) }; }

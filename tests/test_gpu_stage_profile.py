@@ -23,7 +23,11 @@ from gpu_harness import dev, gpu_state
 pytestmark = pytest.mark.gpu
 
 STAGES = ["contact", "car-arena", "ball", "finish", "boost-pads"]
-SPAN_LOW, SPAN_HIGH = 0.95, 1.01
+# The clock span runs from the first workgroup's first clock read to the last
+# workgroup's last one; the launch time adds the dispatch before the first
+# wave and the drain after the last (a few us, 95% of an 80 us tick was seen
+# to dip to 94.9%).
+SPAN_LOW, SPAN_HIGH = 0.90, 1.01
 
 
 def _env(n, n_blue, n_orange, frameskip, seed, window=64, streams=1):
