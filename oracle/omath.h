@@ -26,10 +26,10 @@
  * isolated contacts, the game's published control numbers (jump, dodge, flip,
  * air control, drive and brake, steering radius, autoroll) and brute-force
  * contact geometry (clip polygons, edge closest points, support corners, the
- * kept manifold contact) (tests/).
- * PARITY UNPINNED (no independent check; engine and oracle agree with each
- * other only): the car-side seam adjustment for non-coplanar internal edges;
- * the powerslide steering blend and lateral friction under slip.
+ * kept manifold contact, seam normals at coplanar and angled mesh edges), the
+ * handbrake's rise and fall, the powerslide steer blend measured from the
+ * front axle's impulse direction, and the wheels' slip- and handbrake-scaled
+ * friction (tests/).  Every function of the oracle has such a check.
  */
 #ifndef CARL_ORACLE_MATH_H
 #define CARL_ORACLE_MATH_H

@@ -28,6 +28,13 @@ run that changes only the control under test):
                  THROTTLE_GROUND_ACCEL = 1600 uu/s^2 scaled by the drive curve
                  1 - 0.9 v/1400, to the 1410 uu/s top speed (Drive.cuh:28-66,
                  RLConstants.cuh:270-278)
+  powerslide     the handbrake value rises at 5/s and falls at 2/s; the front
+                 wheels turn by the normal full-lock angle moved toward the
+                 powerslide angle by the handbrake value (read from the
+                 direction of the front axle's impulse); the wheels keep a
+                 lateral friction 1 - 0.8 c scaled by 1 - 0.9 h and a
+                 longitudinal 1 + (0.5 + 0.4 c - 1) h for slip curve input c,
+                 used in the following tick (CarSuspension.cuh:150-190)
 
 Each expected value is computed here from those constants, in float64, so
 a plausible slip in the oracle (a constant swapped between two dodges, the
@@ -493,3 +500,144 @@ def test_no_autoroll_on_four_wheels():
     np.testing.assert_allclose(out[1][0], out[0][0], atol=1e-6)
     np.testing.assert_allclose(out[1][1], out[0][1], atol=1e-7)
     s.close()
+
+
+# ------------------------------------------------------------------ powerslide
+
+POWERSLIDE_RISE, POWERSLIDE_FALL = 5.0, 2.0      # POWERSLIDE_RISE_RATE / _FALL_RATE (RLConstants.cuh:185-186)
+_SLIDE_CURVE = ((0.0, 0.39235), (2500.0, 0.12610))
+
+
+def _slide_angle(speed: float) -> float:
+    """Published front-wheel steer angle at full lock under full handbrake
+    (RLConstants.cuh:263-268)."""
+    (a, fa), (b, fb) = _SLIDE_CURVE
+    if speed <= a:
+        return fa
+    return fa + (fb - fa) * min(speed, b) / b
+
+
+def test_handbrake_rises_and_falls_at_the_published_rates():
+    """Powerslide held, the handbrake value climbs at 5 per second to 1;
+    released, it falls at 2 per second to 0 (Drive.cuh:123-146)."""
+    s = _settled_car()
+    h = 0.0
+    for t in range(40):
+        tick_direct(s, direct(slide=1))
+        h = min(1.0, h + POWERSLIDE_RISE * DT)
+        assert abs(s.car_float("CARL_CAR_HANDBRAKE", 0) - h) < 1e-5, t
+    for t in range(70):
+        tick_direct(s, direct())
+        h = max(0.0, h - POWERSLIDE_FALL * DT)
+        assert abs(s.car_float("CARL_CAR_HANDBRAKE", 0) - h) < 1e-5, t
+    s.close()
+
+
+def _coasting_start(speed: float, handbrake: float, slip: float = 0.0, lat_used: float = 1.0):
+    """A car settled on the flat floor, set moving at `speed` at `slip`
+    radians from its nose, without spin, the handbrake value set, the
+    previous tick's brake, drive and steer cleared and every wheel's
+    friction of the previous tick set to lat_used: no wheel acts along the
+    floor before the first tick's lateral impulses."""
+    s = _settled_car()
+    car, _, _ = s.state()
+    r = rot_matrix(f32(car[s_idx("CARL_CAR_ROT_0"):s_idx("CARL_CAR_ROT_0") + 4, 0]))
+    v = speed * (math.cos(slip) * r[:, 0] + math.sin(slip) * r[:, 1])
+    fields = {("CARL_CAR_VEL_%d" % i, 0): float(v[i]) for i in range(3)}
+    fields.update({("CARL_CAR_ANG_%d" % i, 0): 0.0 for i in range(3)})
+    fields.update({("CARL_CAR_HANDBRAKE", 0): handbrake, ("CARL_CAR_BRAKE_STAGE", 0): 0.0,
+                   ("CARL_CAR_DRIVE_STAGE", 0): 0.0, ("CARL_CAR_STEER_STAGE", 0): 0.0})
+    fields.update({("CARL_CAR_LAT_FRICTION_%d" % w, 0): lat_used for w in range(4)})
+    fields.update({("CARL_CAR_LON_FRICTION_%d" % w, 0): lat_used for w in range(4)})
+    s.set_fields(fields)
+    return s, r
+
+
+def s_idx(name):
+    from test_oracle_physics_pins import CAR
+    return CAR[name]
+
+
+@pytest.mark.parametrize("speed", [300.0, 1200.0, 2200.0])
+@pytest.mark.parametrize("handbrake", [0.5, 1.0])
+@pytest.mark.parametrize("steer", [1.0, -1.0])
+def test_powerslide_blends_the_steer_angle(speed, handbrake, steer):
+    """Under the handbrake the front wheels turn by the normal full-lock
+    angle moved toward the powerslide angle in proportion to the handbrake
+    value: delta = steer x (a(v) + (p(v) - a(v)) h) with a and p the
+    published curves.  Measured from the wheels themselves: a car rolling
+    straight with powerslide held and no throttle gets no brake, drive or
+    rolling friction, so the only impulses along the floor in the tick
+    after the steer is staged are the front wheels' lateral ones, along
+    their axle; the direction of that velocity change is the axle's, turned
+    by delta from the car's right axis."""
+    h0 = handbrake - POWERSLIDE_RISE * DT if handbrake < 1.0 else 1.0
+    s, r0 = _coasting_start(speed, h0)
+    fwd_speed = abs(float(s.car_vec("CARL_CAR_VEL", 0) @ r0[:, 0]))
+    tick_direct(s, direct(slide=1, steer=steer))           # stages the steer angle
+    assert abs(s.car_float("CARL_CAR_HANDBRAKE", 0) - handbrake) < 1e-6
+    car, _, _ = s.state()
+    r = rot_matrix(f32(car[s_idx("CARL_CAR_ROT_0"):s_idx("CARL_CAR_ROT_0") + 4, 0]))
+    v0 = s.car_vec("CARL_CAR_VEL", 0).astype(np.float64)
+    tick_direct(s, direct(slide=1, steer=steer))
+    dv = s.car_vec("CARL_CAR_VEL", 0).astype(np.float64) - v0
+    s.close()
+    dv[2] = 0.0
+    delta = steer * (_steer_angle(fwd_speed) + (_slide_angle(fwd_speed) - _steer_angle(fwd_speed)) * handbrake)
+    right, up = r[:, 1], r[:, 2]
+    axle = right * math.cos(delta) + np.cross(up, right) * math.sin(delta)
+    axle[2] = 0.0
+    axle /= np.linalg.norm(axle)
+    assert np.linalg.norm(dv) > 0.5, dv
+    sin_err = np.linalg.norm(np.cross(dv / np.linalg.norm(dv), axle))
+    assert sin_err < 2e-3, (sin_err, delta, dv)
+
+
+@pytest.mark.parametrize("slip", [0.0, 0.3, 0.8, math.pi / 2])
+@pytest.mark.parametrize("handbrake", [0.0, 0.4, 1.0])
+def test_wheel_friction_under_slip_and_handbrake(slip, handbrake):
+    """The friction each wheel keeps for the next tick (CarSuspension.cuh:
+    150-190): with curve input c = |v.axle| / (|v.(axle x n)| + |v.axle|)
+    for a wheel sliding at slip angle b (c = sin b / (cos b + sin b)), zero
+    below 5 uu/s of side speed, the lateral friction is (1 - 0.8 c) scaled
+    by 1 - 0.9 h under handbrake h, the longitudinal 1 + (0.5 + 0.4 c - 1) h,
+    both x the non-sticky factor (1 on the flat floor).  A car coasting at
+    800 uu/s with the powerslide on (h rises by 5/120 in the tick) or off
+    (falls by 2/120); every wheel's figure is compared."""
+    held = handbrake > 0.0
+    h0 = max(0.0, handbrake - POWERSLIDE_RISE * DT) if held else 0.0
+    s, _ = _coasting_start(800.0, h0, slip)
+    tick_direct(s, direct(slide=1 if held else 0))
+    h = s.car_float("CARL_CAR_HANDBRAKE", 0)
+    assert abs(h - handbrake) < 1e-6
+    side, along = 800.0 * math.sin(slip), 800.0 * math.cos(slip)
+    c = side / (along + side) if side > 5.0 else 0.0
+    lat = (1.0 - 0.8 * c) * (1.0 - 0.9 * h)
+    lon = 1.0 + (0.5 + 0.4 * c - 1.0) * h
+    for w in range(4):
+        got_lat = s.car_float("CARL_CAR_LAT_FRICTION_%d" % w, 0)
+        got_lon = s.car_float("CARL_CAR_LON_FRICTION_%d" % w, 0)
+        assert abs(got_lat - lat) < 3e-3 and abs(got_lon - lon) < 3e-3, (w, got_lat, lat, got_lon, lon)
+    s.close()
+
+
+@pytest.mark.parametrize("slip", [0.5, math.pi / 2])
+def test_lateral_friction_acts_one_tick_later(slip):
+    """The lateral impulse of a tick uses the friction the previous tick
+    kept: two runs differing only in the handbrake value (1 and 0.4 after
+    the first tick) take the same first tick, and in the second the
+    sideways velocity change of the one is (1 - 0.9) / (1 - 0.36) times the
+    other's."""
+    out = []
+    for h in (1.0, 0.4):
+        s, r = _coasting_start(800.0, h - POWERSLIDE_RISE * DT if h < 1.0 else 1.0, slip, lat_used=0.5)
+        v0 = s.car_vec("CARL_CAR_VEL", 0).astype(np.float64)
+        tick_direct(s, direct(slide=1))
+        v1 = s.car_vec("CARL_CAR_VEL", 0).astype(np.float64)
+        tick_direct(s, direct(slide=1))
+        v2 = s.car_vec("CARL_CAR_VEL", 0).astype(np.float64)
+        out.append(((v1 - v0) @ r[:, 1], (v2 - v1) @ r[:, 1]))
+        s.close()
+    (a1, a2), (b1, b2) = out
+    assert a1 == b1 and abs(a1) > 1.0
+    assert abs(a2 / b2 - 0.1 / 0.64) < 2e-3 * 0.1 / 0.64, (a2, b2)
