@@ -27,9 +27,12 @@ constexpr float kCellY = (kArenaMax.y - kArenaMin.y) / 48.f;
 constexpr float kCellZ = (kArenaMax.z - kArenaMin.z) / 10.f;
 constexpr float kBoundaryEdge = 2.f * kPi;
 // ball candidate grid: cubic cells over the broadphase box; a cell lists every
-// triangle whose box comes within ball reach (+1 uu) of the cell
-constexpr float kFineCell = 128.f;
-constexpr int kFineX = 65, kFineY = 94, kFineZ = 17;   // ceil(extent / kFineCell)
+// triangle whose box comes within ball reach (+1 uu) of the cell.  64 uu cells
+// list about half the triangles of 128 uu ones near the curved walls (1.46 M
+// references, 210 MB, against 0.26 M); the cars' contact search, which walks
+// the same lists, runs 3.5% faster per step once cars have spread to the walls.
+constexpr float kFineCell = 64.f;
+constexpr int kFineX = 129, kFineY = 188, kFineZ = 33;   // ceil(extent / kFineCell)
 constexpr int kFineCells = kFineX * kFineY * kFineZ;
 static_assert(kFineX * kFineCell >= kArenaMax.x - kArenaMin.x && kFineY * kFineCell >= kArenaMax.y - kArenaMin.y &&
                   kFineZ * kFineCell >= kArenaMax.z - kArenaMin.z,

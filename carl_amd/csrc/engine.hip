@@ -148,14 +148,20 @@ DI void contactGroup(const Dev& d, const Handoff& out, int screen, int car0, int
         rot = d.cq(CARL_CAR_ROT, car);
         bp = broadphase(d, d.cv(CARL_CAR_POS, car), d.cv(CARL_CAR_VEL, car), d.cv(CARL_CAR_ANG, car), cen, rot);
         demoed = d.ci(CARL_CAR_DEMOED, car) != 0;
-        // the candidate-grid list of the cell holding the car's centre, when
-        // there is one (every triangle within ball reach + 1 uu of the cell,
-        // in ascending triangle order; the car's tests reach less far), else
-        // the broadphase cell's run
+        // the shorter of two lists that both hold every triangle the car can
+        // touch, in ascending triangle order: the candidate-grid list of the
+        // cell holding the car's centre (every triangle within ball reach +
+        // 1 uu of the cell; the car's tests reach less far; its items count
+        // when registered in the broadphase cell), and the broadphase cell's
+        // run itself.  Both orders agree on the triangles that count, so the
+        // tie-breaks by run position pick the same triangle.
         int fcell;
-        fine = ballGridCell(cen, fcell);
-        first = fine ? d.arena.fineStart[fcell] : bp.start;
-        count = fine ? d.arena.fineStart[fcell + 1] - first : bp.count;
+        const bool inGrid = ballGridCell(cen, fcell);
+        const int fFirst = inGrid ? d.arena.fineStart[fcell] : 0;
+        const int fCount = inGrid ? d.arena.fineStart[fcell + 1] - fFirst : 0;
+        fine = inGrid && fCount < bp.count;
+        first = fine ? fFirst : bp.start;
+        count = fine ? fCount : bp.count;
     }
     contactPrepare(L, lane, ok && !demoed, cen, rot, first, fine, bp.cell, screen != 0);
     waveSync();
