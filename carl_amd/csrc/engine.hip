@@ -609,10 +609,14 @@ HDI int packChunkRows(int rowLen)
 }
 HDI size_t packLdsBytes(int rowLen) { return (size_t)packChunkRows(rowLen) * packStride(rowLen) * sizeof(float); }
 
+typedef float F4v __attribute__((ext_vector_type(4)));
+
 // Stores `rows` whole rows (rowLen floats each, row stride `stride` floats in
 // LDS from `lds`) to the contiguous run at dst; 16 bytes per lane and
-// instruction when dst is 16-byte aligned.  Called by every thread of the
-// workgroup.
+// instruction when dst is 16-byte aligned.  The stores are non-temporal: the
+// rows are not read again by the step, and streaming them past the caches
+// keeps the state words the later stages re-read cached (packing 36.6 ->
+// 34.3 us).  Called by every thread of the workgroup.
 DI void storeRunFromLds(float* dst, int rowLen, int stride, int rows, const float* lds)
 {
     const int t = threadIdx.x, total = rows * rowLen;
@@ -627,19 +631,20 @@ DI void storeRunFromLds(float* dst, int rowLen, int stride, int rows, const floa
                 v[k] = lds[r2 * stride + c2];
                 if (++c2 == rowLen) { c2 = 0; r2++; }
             }
-            *reinterpret_cast<float4*>(dst + e) = make_float4(v[0], v[1], v[2], v[3]);
+            const F4v run = { v[0], v[1], v[2], v[3] };
+            __builtin_nontemporal_store(run, reinterpret_cast<F4v*>(dst + e));
             rr += rs;
             c += cs;
             if (c >= rowLen) { c -= rowLen; rr++; }
         }
         const int e = (total & ~3) + t;
-        if (e < total) dst[e] = lds[(e / rowLen) * stride + e % rowLen];
+        if (e < total) __builtin_nontemporal_store(lds[(e / rowLen) * stride + e % rowLen], dst + e);
         return;
     }
     const int rowStep = kPackBlock / rowLen, colStep = kPackBlock % rowLen;
     int rr = t / rowLen, c = t % rowLen;
     for (int e = t; e < total; e += kPackBlock) {
-        dst[e] = lds[rr * stride + c];
+        __builtin_nontemporal_store(lds[rr * stride + c], dst + e);
         rr += rowStep;
         c += colStep;
         if (c >= rowLen) { c -= rowLen; rr++; }
@@ -741,10 +746,26 @@ __global__ __launch_bounds__(kPackBlock) void stepEnvKernel(Dev d, StepIO io)
     const int t = threadIdx.x, lane = t & 63, q = t >> 6, nC = d.nCars;
     const int s0 = blockIdx.x * kStepSims, s1 = min(s0 + kStepSims, d.nSim);
     const int s = s0 + lane;
+    // the match words and the first action words are loaded first and used
+    // after the transition state's loads have been issued
+    MatchWords m{};
+    if (s < s1) m = matchWords(d, s);
+    constexpr int kCopyRegs = 4;   // action words per thread held in registers (all of them in 1v1)
+    const int copyWords = io.actionCopy ? (s1 - s0) * nC * 7 : 0;
+    const size_t w0 = (size_t)s0 * nC * 7;
+    uint32_t act[kCopyRegs];
+#pragma unroll
+    for (int i = 0; i < kCopyRegs; i++) act[i] = t + i * kPackBlock < copyWords ? io.actions[w0 + t + i * kPackBlock] : 0u;
+
+    // round 1: the first chunk of transition state rows, and as many
+    // transition observation rows as fit beside them
+    const int sStride = packStride(io.stateDim), oStride = packStride(io.obsDim);
+    const int aRows = min(packChunkRows(io.stateDim), s1 - s0);
+    if (lane < aRows) packStatePart(d, s0 + lane, io.frameskip, io.tickCount, q, packLds + lane * sStride);
+
     int outcome = kKept;
     bool dn = false;
     if (s < s1) {
-        const MatchWords m = matchWords(d, s);
         dn = simDoneFrom(m, io.tickCount, io.rule);
         outcome = doneOutcome(m, io.tickCount, io.rule);
         if (q == 0) {
@@ -758,25 +779,15 @@ __global__ __launch_bounds__(kPackBlock) void stepEnvKernel(Dev d, StepIO io)
             io.overtime[s] = outcome == kReset ? false : (outcome == kOvertimeEntered || m.overtime != 0);
         }
     }
-    if (io.actionCopy) {
-        const size_t w0 = (size_t)s0 * nC * 7;
-        for (int w = t; w < (s1 - s0) * nC * 7; w += kPackBlock) io.actionCopy[w0 + w] = io.actions[w0 + w];
-    }
     // the finished simulations, the same mask in every wave; the transition
     // observation rows of finished simulation j (in lane order) are
     // doneRank(j) * nC .. + nC - 1
     const uint64_t doneMask = __ballot(dn);
     const int doneRows = __popcll(doneMask) * nC;
     auto doneRank = [&](int local) { return __popcll(doneMask & ((1ull << local) - 1ull)); };
-
-    // round 1: the first chunk of transition state rows, and as many
-    // transition observation rows as fit beside them
-    const int sStride = packStride(io.stateDim), oStride = packStride(io.obsDim);
-    const int aRows = min(packChunkRows(io.stateDim), s1 - s0);
     float* const ldsB = packLds + aRows * sStride;
     const int capB = ((int)(stepLdsBytes(io.obsDim, io.stateDim) / sizeof(float)) - aRows * sStride) / oStride;
     const int nB = min(doneRows, max(capB, 0));
-    if (lane < aRows) packStatePart(d, s0 + lane, io.frameskip, io.tickCount, q, packLds + lane * sStride);
     if (lane < nB) {
         // the lane-th finished row: its simulation is the (lane / nC)-th set bit of doneMask
         uint64_t m = doneMask;
@@ -825,6 +836,11 @@ __global__ __launch_bounds__(kPackBlock) void stepEnvKernel(Dev d, StepIO io)
     packRowsParts(
         io.state, io.stateDim, s0, s1, [](int) { return true; },
         [&](int r, int qq, float* o) { packStatePart(d, r, 1, io.tickCount, qq, o); });
+    // the kept copy of the step's actions
+#pragma unroll
+    for (int i = 0; i < kCopyRegs; i++)
+        if (t + i * kPackBlock < copyWords) io.actionCopy[w0 + t + i * kPackBlock] = act[i];
+    for (int w = t + kCopyRegs * kPackBlock; w < copyWords; w += kPackBlock) io.actionCopy[w0 + w] = io.actions[w0 + w];
 }
 
 __global__ void setBallKernel(Dev d, const float* pos, const float* vel, const float* ang, Selection sel)
