@@ -137,11 +137,15 @@ DI bool rayBox(V3 start, V3 dir, V3 center, Q4 rot, float maxDist, float& dist, 
 DI void raycastBodies(const Dev& d, int car, int sim, const V3* start, V3 dir, Wheels& w)
 {
     const int base = sim * d.nCars;
+    const V3 ball = d.sv(CARL_SIM_BALL_POS, sim);
     for (int o = 0; o < d.nCars; o++) {
         const int oc = base + o;
-        if (oc == car || d.ci(CARL_CAR_DEMOED, oc)) continue;
+        // the other car's words are loaded together, before its demolished
+        // flag is tested (one round trip instead of two)
+        const int demoed = d.ci(CARL_CAR_DEMOED, oc);
         const V3 ocen = d.cv(CARL_CAR_CEN, oc);
         const Q4 orot = d.cq(CARL_CAR_ROT, oc);
+        if (oc == car || demoed) continue;
 #pragma unroll
         for (int k = 0; k < kWheels; k++) {
             float dd;
@@ -152,7 +156,6 @@ DI void raycastBodies(const Dev& d, int car, int sim, const V3* start, V3 dir, W
             w.src[k] = kSrcCar;
         }
     }
-    const V3 ball = d.sv(CARL_SIM_BALL_POS, sim);
     const float invR = 1.f / kBallRadius;
 #pragma unroll
     for (int k = 0; k < kWheels; k++) {
@@ -1106,6 +1109,9 @@ DI void contactHeavy(const Dev& d, ContactLdsT<Owners>& L, int lane)
         const int ref = L.first[o] + q;
         const bool fine = L.fine[o] != 0;
         const Tri t = unpackTri((fine ? d.arena.fineRec : d.arena.rec) + 4 * (size_t)ref);
+        // the edge angles a contact's edge adjustment needs, loaded with the
+        // triangle (one round trip instead of two)
+        const float4 ang = fine ? d.arena.fineAux[ref] : d.arena.refAng[ref];
         const V3 dir = ownerDir(L, o);
         const V3 pv = cross(dir, t.e2);
         const float det = dot(t.e1, pv);
@@ -1169,7 +1175,6 @@ DI void contactHeavy(const Dev& d, ContactLdsT<Owners>& L, int lane)
             if (triBestContact(lt, sat, near, L.nearN[o], c, value)) {
                 atomicMin(&L.bestKey[o], contactKey(value, q));
                 const Q4 rot{ L.rot[0][o], L.rot[1][o], L.rot[2][o], L.rot[3][o] };
-                const float4 ang = fine ? d.arena.fineAux[ref] : d.arena.refAng[ref];
                 adjustEdgeContact(lt, V3{ ang.x, ang.y, ang.z }, c);
                 manPt = ManPt{ c.carPos, ownerCen(L, o) + rotate(rot, c.arenaPos), rotate(rot, c.normal), -c.depth };
                 hasContact = true;
