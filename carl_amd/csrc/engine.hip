@@ -743,6 +743,7 @@ HDI size_t stepLdsBytes(int obsDim, int stateDim)
 __global__ __launch_bounds__(kPackBlock) void stepEnvKernel(Dev d, StepIO io)
 {
     extern __shared__ float packLds[];
+    __shared__ int listedRow[64];   // tobs row of each transition observation built in round 1
     const int t = threadIdx.x, lane = t & 63, q = t >> 6, nC = d.nCars;
     const int s0 = blockIdx.x * kStepSims, s1 = min(s0 + kStepSims, d.nSim);
     const int s = s0 + lane;
@@ -787,7 +788,7 @@ __global__ __launch_bounds__(kPackBlock) void stepEnvKernel(Dev d, StepIO io)
     auto doneRank = [&](int local) { return __popcll(doneMask & ((1ull << local) - 1ull)); };
     float* const ldsB = packLds + aRows * sStride;
     const int capB = ((int)(stepLdsBytes(io.obsDim, io.stateDim) / sizeof(float)) - aRows * sStride) / oStride;
-    const int nB = min(doneRows, max(capB, 0));
+    const int nB = min(doneRows, min(max(capB, 0), 64));   // listedRow holds 64
     if (lane < nB) {
         // the lane-th finished row: its simulation is the (lane / nC)-th set bit of doneMask
         uint64_t m = doneMask;
@@ -795,6 +796,7 @@ __global__ __launch_bounds__(kPackBlock) void stepEnvKernel(Dev d, StepIO io)
         const int local = __ffsll((unsigned long long)m) - 1;
         packObservationPart(d, s0 + local, lane % nC, io.invert != 0, io.normalize != 0, io.prev != 0, q,
                             ldsB + lane * oStride);
+        if (q == 0) listedRow[lane] = (s0 + local) * nC + lane % nC;
     }
     __syncthreads();
     storeRunFromLds(io.tstate + (size_t)s0 * io.stateDim, io.stateDim, sStride, aRows, packLds);
@@ -803,10 +805,7 @@ __global__ __launch_bounds__(kPackBlock) void stepEnvKernel(Dev d, StepIO io)
         const int total = nB * io.obsDim;
         for (int e = t; e < total; e += kPackBlock) {
             const int j = e / io.obsDim, c = e % io.obsDim;
-            uint64_t m = doneMask;
-            for (int k = 0; k < j / nC; k++) m &= m - 1ull;
-            const int row = (s0 + __ffsll((unsigned long long)m) - 1) * nC + j % nC;
-            io.tobs[(size_t)row * io.obsDim + c] = ldsB[j * oStride + c];
+            __builtin_nontemporal_store(ldsB[j * oStride + c], io.tobs + (size_t)listedRow[j] * io.obsDim + c);
         }
     }
     __syncthreads();
