@@ -196,7 +196,7 @@ std::string buildArena(const std::string& objPath, HostArena& out)
     }
 
     // device records, per triangle and per cell reference
-    if (nTris >= kMaxArenaTris) return "arena mesh has more than 2^24 triangles";
+    if (nTris >= kMaxArenaTris) return "arena mesh has more than 2^23 triangles";
     out.triRecords.assign(16 * (size_t)nTris, 0.f);
     const int nRefs = out.cellStart[kCells];
     out.records.assign(16 * (size_t)nRefs, 0.f);

@@ -969,6 +969,8 @@ constexpr float kHalfLen = 80.f;               // |kHalf| rounded up
 // registers; the tick-window kernel searches a whole wave of cars at once.
 constexpr int kContactOwners = 32;
 
+constexpr int kQueueSat = 1 << 23;   // queue entry flag; item positions stay below it (kMaxArenaTris)
+
 template <int Owners>
 struct ContactLdsT {
     int excl[64];
@@ -988,7 +990,8 @@ struct ContactLdsT {
     unsigned long long bestKey[Owners];
     float rayNrm[kWheels][3][Owners];   // surface normal of each wheel's nearest arena hit
     float bestPt[10][Owners];           // manifold point of the deepest arena contact so far
-    // screened items in run order, entries owner << 24 | item
+    // screened items in run order, entries owner << 24 | kQueueSat (the SAT
+    // may accept it) | item
     int candQ[128];
     int candN;
 };
@@ -1084,7 +1087,10 @@ DI void contactScreen(ContactLdsT<Owners>& L, const RefBox& b, int o, int q, int
     const bool keep = b.live && (s4.z == 0.f || !(satMiss && rayMiss));
     const unsigned long long m = __ballot(keep);
     const int n0 = L.candN;
-    if (keep) L.candQ[n0 + __popcll(m & lanesBelow(lane))] = (o << 24) | q;
+    // bit 23: the SAT may accept the item (the screen could not prove it
+    // rejects; only the rays keep the others)
+    const int satBit = (s4.z == 0.f || !satMiss) ? kQueueSat : 0;
+    if (keep) L.candQ[n0 + __popcll(m & lanesBelow(lane))] = (o << 24) | satBit | q;
     if (lane == (int)__builtin_ctzll(__ballot(1))) L.candN = n0 + __popcll(m);
 }
 
@@ -1100,7 +1106,8 @@ DI void contactHeavy(const Dev& d, ContactLdsT<Owners>& L, int lane)
     const int take = n < 64 ? n : 64;
     const bool active = lane < take;
     const int e = active ? L.candQ[lane] : 0;
-    const int o = e >> 24, q = e & 0xffffff;
+    const int o = e >> 24, q = e & (kQueueSat - 1);
+    const bool satNeeded = (e & kQueueSat) != 0;
     bool rayHit = false;
     V3 fn = kZero;   // surface normal facing against the rays, for lanes with a ray hit
     bool hasContact = false;
@@ -1150,7 +1157,7 @@ DI void contactHeavy(const Dev& d, ContactLdsT<Owners>& L, int lane)
         bool hit = false;
         LocalTri lt;
         Sat sat;
-        if (L.satOn[o] && !t.plane) {
+        if (L.satOn[o] && !t.plane && satNeeded) {
             const Q4 rot{ L.rot[0][o], L.rot[1][o], L.rot[2][o], L.rot[3][o] };
             lt = toLocal(t, ownerCen(L, o), rot);
             sat = boxTriSat(lt);

@@ -30,7 +30,7 @@ namespace carl {
 
 constexpr uint32_t kPlaneFlag = 0x80000000u;  // analytic plane triangle: skipped by the car SAT
 
-constexpr int kMaxArenaTris = 1 << 24;  // contact-search queue entries keep a run position in 24 bits
+constexpr int kMaxArenaTris = 1 << 23;  // contact-search queue entries keep a run position in 23 bits
 
 struct ArenaView {
     const float4* rec;       // 4 per cell reference
