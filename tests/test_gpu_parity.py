@@ -107,12 +107,15 @@ def test_clustered_3v3_contacts(gpu):
     p.close()
 
 
-@pytest.mark.parametrize("n_blue,frameskip", [(1, 8), (2, 1)])
+@pytest.mark.parametrize("n_blue,frameskip", [(1, 8), (2, 1), (3, 4), (4, 2)])
 def test_short_episodes_timeouts_overtime_and_resets(gpu, n_blue, frameskip):
     """Episodes of a few steps: regulation timeouts, ties that enter overtime,
     overtime expiry and no-touch timeouts end simulations on most steps, so
     the packing's reset decisions, the match state after the resets and the
-    transition rows of finished simulations all run against the oracle."""
+    transition rows of finished simulations all run against the oracle.  In
+    3v3 and 4v4 the state rows take more than one LDS chunk and only a few
+    finished rows fit beside the first, so the packing's further rounds for
+    both run too (96 simulations: one full packing workgroup and one partial)."""
     rng = np.random.default_rng(18 + n_blue)
     n, nc = 96, 2 * n_blue
     p = Pair(n, n_blue, n_blue, seed=12, frameskip=frameskip)
