@@ -601,11 +601,14 @@ constexpr int kPackBlock = 64 * kRowParts;
 constexpr int kPackLdsBytes = 38 * 1024;   // four workgroups per CU
 
 HDI int packStride(int rowLen) { return rowLen | 1; }
+// Rows per LDS chunk: as many as fit kPackLdsBytes, at most 64 and a
+// multiple of 4 (a chunk's first row then starts 16-byte aligned in the
+// output whenever the row length is even), at least 8.
 HDI int packChunkRows(int rowLen)
 {
-    int rows = 64;
-    while (rows > 8 && rows * packStride(rowLen) * 4 > kPackLdsBytes) rows /= 2;
-    return rows;
+    const int fit = kPackLdsBytes / (packStride(rowLen) * 4);
+    const int rows = (fit < 64 ? fit : 64) & ~3;
+    return rows > 8 ? rows : 8;
 }
 HDI size_t packLdsBytes(int rowLen) { return (size_t)packChunkRows(rowLen) * packStride(rowLen) * sizeof(float); }
 
@@ -761,7 +764,11 @@ __global__ __launch_bounds__(kPackBlock) void stepEnvKernel(Dev d, StepIO io)
     // round 1: the first chunk of transition state rows, and as many
     // transition observation rows as fit beside them
     const int sStride = packStride(io.stateDim), oStride = packStride(io.obsDim);
-    const int aRows = min(packChunkRows(io.stateDim), s1 - s0);
+    // when the state rows take several chunks, the first one is an even
+    // share (a multiple of 4), which leaves LDS for more transition
+    // observations beside it
+    const int sChunk = packChunkRows(io.stateDim), sChunks = (s1 - s0 + sChunk - 1) / sChunk;
+    const int aRows = min((((s1 - s0 + sChunks - 1) / sChunks) + 3) & ~3, min(sChunk, s1 - s0));
     if (lane < aRows) packStatePart(d, s0 + lane, io.frameskip, io.tickCount, q, packLds + lane * sStride);
 
     int outcome = kKept;
