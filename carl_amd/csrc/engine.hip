@@ -384,6 +384,7 @@ __global__ __launch_bounds__(kTickBlock) void finishKernel(Dev d, int simsPerBlo
 constexpr int kWindowBlock = CARL_WINDOW_BLOCK;
 constexpr int kWindowWaves = kWindowBlock / 64;
 constexpr int kDefaultWindowSims = CARL_WINDOW_SIMS;
+constexpr int kAutoWindowMin = 8;   // smallest automatic window workgroup (simulations)
 // rounds of candidate loads the window kernel's contact search keeps in flight
 #ifndef CARL_WINDOW_CONTACT_DEPTH
 #define CARL_WINDOW_CONTACT_DEPTH 1
@@ -1096,6 +1097,12 @@ struct carl_env {
     hipStream_t aux[kMaxTickStreams - 1] = {};
     hipEvent_t fork = nullptr, join[kMaxTickStreams - 1] = {};
     int windowSims = kDefaultWindowSims;  // simulations per block of the tick-window kernel (0: phase kernels)
+    // Until the caller sets windowSims, a run too small to fill the device's
+    // resident window workgroups uses smaller ones (down to kAutoWindowMin
+    // simulations): the kernel's time is one workgroup's latency chain, so
+    // spreading the simulations over more compute units shortens it.
+    bool windowAuto = true;
+    int windowResident = 0;   // window workgroups the device holds at once
     int timing = 0;                      // CARL_TIME_* flags
     // timing: a start and an end event per timed launch not yet folded
     // (a pool of at most kTimedPool pairs) and the launch's kernel id;
@@ -1252,7 +1259,10 @@ int launchTicks(carl_env* e, int kind, const void* actions, int n)
         for (int p = 1; p < parts; p++) HIP_TRY(hipStreamWaitEvent(stream[p], e->fork, 0));
     }
     if (e->windowSims > 0) {
-        const int wsb = std::min(e->windowSims, kWindowBlock / e->nCars);
+        int wsb = std::min(e->windowSims, kWindowBlock / e->nCars);
+        if (e->windowAuto)
+            while (wsb / 2 >= kAutoWindowMin && e->grid(range[0].end - range[0].begin, wsb / 2) <= e->windowResident)
+                wsb /= 2;
         for (int p = 0; p < parts; p++) {
             const SimRange r = range[p];
             const bool timed = p == 0;
@@ -1462,6 +1472,15 @@ int carl_env_create(int nSim, int nBlue, int nOrange, int seed, int frameskip, i
         if (hipStreamCreateWithFlags(&e->aux[i], hipStreamNonBlocking) != hipSuccess
             || hipEventCreateWithFlags(&e->join[i], hipEventDisableTiming) != hipSuccess)
             return bail(fail(CARL_ERR_RUNTIME, "hipStreamCreate failed"));
+    }
+    {
+        int device = 0, cus = 0, perCu = 0;
+        if (hipGetDevice(&device) != hipSuccess
+            || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess
+            || hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                   &perCu, e->nCars == 2 ? tickWindowKernel<2> : tickWindowKernel<0>, kWindowBlock, 0) != hipSuccess)
+            return bail(fail(CARL_ERR_RUNTIME, "window kernel occupancy query failed"));
+        e->windowResident = perCu * cus;
     }
     const size_t nT = (size_t)e->nTotal, nS = (size_t)nSim;
     int rc = CARL_OK;
@@ -1728,6 +1747,7 @@ int carl_env_set_param(carl_env* e, int p, int v)
     case CARL_PARAM_TICK_WINDOW:
         if (v < 0 || v > kWindowBlock) return fail(CARL_ERR_VALUE, "tick_window must be in [0, 128]");
         e->windowSims = v;
+        e->windowAuto = false;
         return CARL_OK;
     default: return fail(CARL_ERR_VALUE, "parameter is read-only or unknown");
     }
