@@ -123,8 +123,10 @@ enum {
                                       provably reject before running them; 0: it runs them on every pair.
                                       Results are identical; no reference counterpart (default 1) */
     CARL_PARAM_TICK_WINDOW = 13,   /* > 0: all ticks of a step in one launch per partition, this many
-                                      simulations per workgroup (at most 128 cars; default 64); 0: four phase kernels
-                                      per tick.  Results are identical; no reference counterpart */
+                                      simulations per workgroup (at most 128 cars; default 64, halved down
+                                      to 8 for runs too small to fill the GPU until it is set); 0: four
+                                      phase kernels per tick.  Results are identical; no reference
+                                      counterpart */
     CARL_PARAM_NATIVE_ARENA = 14   /* read-only: 1 when the environment was created with native mesh
                                       metadata (the reference's ArenaMesh::hasNativeMetadata) */
 };
