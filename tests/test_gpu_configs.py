@@ -156,6 +156,8 @@ def test_turtle_recovery_one_car(gpu, jump):
     (3, 2, True, False, True, True),
     (1, 1, False, True, False, False),
     (2, 1, False, False, False, True),
+    (3, 3, True, True, False, False),
+    (4, 3, True, True, True, False),
 ])
 def test_creation_options_stepping(gpu, n_blue, n_orange, invert, normalize, previous, discrete):
     """Observations without orange inversion, normalised, with the previous
