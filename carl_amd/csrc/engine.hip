@@ -528,7 +528,7 @@ DI void tickWindowBody(Dev d0, uint32_t* __restrict__ ws, int screen, int kind, 
 // two waves per SIMD (the second bound is waves per execution unit): 256
 // VGPRs.  Cars > 0: instantiated for that many cars per simulation (1v1, the
 // common case, measured 6% faster than the same kernel with the count
-// read at run time); 0: any count.
+// read at run time; 2v2 and 3v3 5% and 3%); 0: any count.
 template <int Cars>
 __global__ __launch_bounds__(kWindowBlock, 2) void tickWindowKernel(Dev d, uint32_t* __restrict__ ws, int screen,
                                                                  int kind, const void* __restrict__ actions,
@@ -536,6 +536,19 @@ __global__ __launch_bounds__(kWindowBlock, 2) void tickWindowKernel(Dev d, uint3
                                                                  SimRange range)
 {
     tickWindowBody<false, false, Cars>(d, ws, screen, kind, actions, tick0, ticks, simsPerBlock, range, nullptr);
+}
+
+using WindowKernel = void (*)(Dev, uint32_t*, int, int, const void*, int, int, int, SimRange);
+
+// the instance for a car count: 1v1, 2v2 and 3v3 have their own
+WindowKernel windowKernelFor(int nCars)
+{
+    switch (nCars) {
+    case 2: return tickWindowKernel<2>;
+    case 4: return tickWindowKernel<4>;
+    case 6: return tickWindowKernel<6>;
+    default: return tickWindowKernel<0>;
+    }
 }
 
 // the same with the native arena meshes
@@ -1279,9 +1292,7 @@ int launchTicks(carl_env* e, int kind, const void* actions, int n)
                                      e->tickCount + 1, n, wsb, r, e->prof));
             } else {
                 CARL_MARK(launchTick(e, timed, CARL_KERNEL_WINDOW,
-                                     e->nativeRec      ? tickWindowNativeKernel
-                                     : e->nCars == 2   ? tickWindowKernel<2>
-                                                       : tickWindowKernel<0>,
+                                     e->nativeRec ? tickWindowNativeKernel : windowKernelFor(e->nCars),
                                      dim3(blocks),
                                      dim3(kWindowBlock), 0, stream[p], d, e->ws, e->contactScreen, kind, actions,
                                      e->tickCount + 1, n, wsb, r));
@@ -1478,7 +1489,7 @@ int carl_env_create(int nSim, int nBlue, int nOrange, int seed, int frameskip, i
         if (hipGetDevice(&device) != hipSuccess
             || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess
             || hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                   &perCu, e->nCars == 2 ? tickWindowKernel<2> : tickWindowKernel<0>, kWindowBlock, 0) != hipSuccess)
+                   &perCu, windowKernelFor(e->nCars), kWindowBlock, 0) != hipSuccess)
             return bail(fail(CARL_ERR_RUNTIME, "window kernel occupancy query failed"));
         e->windowResident = perCu * cus;
     }
