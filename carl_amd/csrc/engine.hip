@@ -479,8 +479,15 @@ DI void tickWindowBody(Dev d0, uint32_t* __restrict__ ws, int screen, int kind, 
             carArenaCar(d, LdsHandoff{ L.wave[wave].hand }, kind, actions, tick, c, lane);
         __syncthreads();
         mark(kStageCarArena);
-        for (int g = sim0 + wave * kBallOwners; g < simEnd; g += kWindowWaves * kBallOwners)
-            ballGroup<Native>(d, tick, g, simEnd, L.wave[wave].ball, lane);
+        {
+            // the block's simulations split evenly between the waves (a
+            // block of 21 3v3 or 32 2v2 simulations would otherwise leave
+            // the second wave idle): at most kBallOwners per wave and group
+            const int per = (simEnd - sim0 + kWindowWaves - 1) / kWindowWaves;
+            const int wEnd = min(sim0 + (wave + 1) * per, simEnd);
+            for (int g = sim0 + wave * per; g < wEnd; g += kBallOwners)
+                ballGroup<Native>(d, tick, g, min(g + kBallOwners, wEnd), L.wave[wave].ball, lane);
+        }
         __syncthreads();
         mark(kStageBall);
         for (int c = car0 + t; c < carEnd; c += kWindowBlock) finishCar(d, c);
