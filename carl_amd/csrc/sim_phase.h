@@ -1089,15 +1089,19 @@ DI float extraCurve(float s)
     return 0.30f;
 }
 
-// one ball-car contact solve, split correction and extra impulse (CarBall/Solve.cuh:207-243)
-DI void ballCarPair(const Dev& d, int sim, int c, V3 preBallVel, int tick)
+// one ball-car contact solve, split correction and extra impulse
+// (CarBall/Solve.cuh:207-243) for a car that is not demolished.  The ball's
+// position and velocities are the caller's registers, updated in place (the
+// caller stores them); every word of the car the pair reads, and the ball's
+// accumulated impulse, is loaded in one batch before any is tested.
+DI void ballCarPair(const Dev& d, int sim, int c, V3 preBallVel, int tick, V3& ballNow, V3& bv, V3& ba)
 {
-    if (d.ci(CARL_CAR_DEMOED, c)) return;
-    const V3 ballPos = d.sv(CARL_SIM_BALL_POS, sim);
-    V3 bv = d.sv(CARL_SIM_BALL_VEL, sim), ba = d.sv(CARL_SIM_BALL_ANG, sim);
     const V3 carPos = d.cv(CARL_CAR_POS, c), carCen = d.cv(CARL_CAR_CEN, c);
     V3 cv = d.cv(CARL_CAR_VEL, c), ca = d.cv(CARL_CAR_ANG, c);
     const Q4 rot = d.cq(CARL_CAR_ROT, c);
+    const int last = d.ci(CARL_CAR_BALL_HIT_TICK, c);
+    const V3 ballImp = d.sv(CARL_SIM_BALL_IMP, sim);
+    const V3 ballPos = ballNow;
     const V3 preCarVel = cv;
 
     const V3 core{ kHalf.x - kCarMargin, kHalf.y - kCarMargin, kHalf.z - kCarMargin };
@@ -1153,15 +1157,13 @@ DI void ballCarPair(const Dev& d, int sim, int c, V3 preBallVel, int tick)
         cv = cv - fr.axis * (fi * kCarInvMass);
         ca = ca - fr.carAngular * fi;
     }
-    d.ssetv(CARL_SIM_BALL_VEL, sim, bv);
-    d.ssetv(CARL_SIM_BALL_ANG, sim, ba);
     d.setv(CARL_CAR_VEL, c, cv);
     d.setv(CARL_CAR_ANG, c, ca);
 
     const float pen = depth - kLinearSlop;
     if (pen > 0.f) {
         const float push = pen * kContactErp / kDt * nr.jacInv;
-        d.ssetv(CARL_SIM_BALL_POS, sim, d.sv(CARL_SIM_BALL_POS, sim) + normal * (push * kBallInvMass * kDt));
+        ballNow = ballPos + normal * (push * kBallInvMass * kDt);
         const V3 np = carPos + normal * (-push * kCarInvMass * kDt);
         const Q4 nrot = integrateRotation(rot, (nr.carAngular * -push) * kSplitTurnErp);
         d.setv(CARL_CAR_POS, c, np);
@@ -1171,7 +1173,6 @@ DI void ballCarPair(const Dev& d, int sim, int c, V3 preBallVel, int tick)
 
     d.seti(CARL_CAR_BALL_CONTACT_TICK, c, tick);
     d.sseti(CARL_SIM_LAST_TOUCH_TICK, sim, tick);
-    const int last = d.ci(CARL_CAR_BALL_HIT_TICK, c);
     if (tick <= last + 1 && last <= tick) return;
     d.seti(CARL_CAR_BALL_HIT_TICK, c, tick);
     const V3 relVel = preBallVel - preCarVel;
@@ -1190,7 +1191,7 @@ DI void ballCarPair(const Dev& d, int sim, int c, V3 preBallVel, int tick)
             added = hd * (speed * extraCurve(speed));
         }
     }
-    d.ssetv(CARL_SIM_BALL_IMP, sim, d.sv(CARL_SIM_BALL_IMP, sim) + added);
+    d.ssetv(CARL_SIM_BALL_IMP, sim, ballImp + added);
 }
 
 // drag, arena solve, car contacts, integration in Bullet units and goal check
@@ -1201,53 +1202,56 @@ DI bool ballSleeping(const Dev& d, int sim)
 }
 
 // solveArena(body, wasHit): the ball-arena solve at the exported ball
-// position (not called when the ball sleeps)
+// position (not called when the ball sleeps).  Every word the tick tests is
+// loaded in one batch before any test (the hit ticks and the near-car tests
+// read car words that nothing before their use changes in this phase: the
+// car-car pairs have run, and a car-ball pair writes only its own car); the
+// ball's position and velocities then stay in registers through the car
+// pairs and are stored once.
 template <class SolveArena>
 DI void ballTickWith(const Dev& d, int sim, int tick, SolveArena solveArena)
 {
     const V3 ballVel = d.sv(CARL_SIM_BALL_VEL, sim), ballAng = d.sv(CARL_SIM_BALL_ANG, sim);
-    const bool sleeping = lensq(ballVel) == 0.f && lensq(ballAng) == 0.f;
     const V3 exported = d.sv(CARL_SIM_BALL_POS, sim);
     const bool valid = d.si(CARL_SIM_BALL_INT_VALID, sim) != 0;
-    V3 posBT = (valid && lensq(exported - d.sv(CARL_SIM_BALL_EXP_POS, sim)) == 0.f) ? d.sv(CARL_SIM_BALL_INT_POS, sim)
-                                                                                      : exported * .02f;
-    V3 velBT = (valid && lensq(ballVel - d.sv(CARL_SIM_BALL_EXP_VEL, sim)) == 0.f) ? d.sv(CARL_SIM_BALL_INT_VEL, sim)
-                                                                                    : ballVel * .02f;
+    const V3 expPos = d.sv(CARL_SIM_BALL_EXP_POS, sim), intPos = d.sv(CARL_SIM_BALL_INT_POS, sim);
+    const V3 expVel = d.sv(CARL_SIM_BALL_EXP_VEL, sim), intVel = d.sv(CARL_SIM_BALL_INT_VEL, sim);
+    const int base = sim * d.nCars;
+    const V3 solverHalf{ kHalf.x + kCarMargin, kHalf.y + kCarMargin, kHalf.z + kCarMargin };
+    const float maxDist = kBallRadius + len(solverHalf);
+    bool hit = false;
+    unsigned near = 0;
+    for (int k = 0; k < d.nCars; k++) {
+        const int h = d.ci(CARL_CAR_BALL_HIT_TICK, base + k);
+        const bool demoed = d.ci(CARL_CAR_DEMOED, base + k) != 0;
+        const V3 cen = d.cv(CARL_CAR_CEN, base + k);
+        hit |= h >= 0 && tick > 0 && h == tick - 1;
+        if (!demoed && !(lensq(exported - cen) > maxDist * maxDist)) near |= 1u << k;
+    }
+    const bool sleeping = lensq(ballVel) == 0.f && lensq(ballAng) == 0.f;
+    V3 posBT = (valid && lensq(exported - expPos) == 0.f) ? intPos : exported * .02f;
+    V3 velBT = (valid && lensq(ballVel - expVel) == 0.f) ? intVel : ballVel * .02f;
     const V3 damped = sleeping ? velBT : velBT * kBallDrag;
     const V3 preBT = sleeping ? velBT : damped + (kGravity * .02f) * kDt;
     const V3 velNoExt = damped * 50.f;
     const V3 preVel = preBT * 50.f;
     V3 pushVel = kZero;
-    const int base = sim * d.nCars;
+    V3 pos = exported, vel = ballVel, ang = ballAng;
     if (!sleeping) {
-        bool hit = false;
-        for (int k = 0; k < d.nCars; k++) {
-            const int h = d.ci(CARL_CAR_BALL_HIT_TICK, base + k);
-            hit |= h >= 0 && tick > 0 && h == tick - 1;
-        }
         BallBody b;
         b.vel = preVel; b.velNoExt = velNoExt; b.ang = ballAng;
         b.dVel = kZero; b.dAng = kZero; b.pushVel = kZero; b.pushAng = kZero;
         solveArena(b, hit);
-        d.ssetv(CARL_SIM_BALL_VEL, sim, b.vel);
-        d.ssetv(CARL_SIM_BALL_ANG, sim, b.ang);
+        vel = b.vel;
+        ang = b.ang;
         pushVel = b.pushVel;
     }
-    {
-        const V3 bp = d.sv(CARL_SIM_BALL_POS, sim);
-        const V3 solverHalf{ kHalf.x + kCarMargin, kHalf.y + kCarMargin, kHalf.z + kCarMargin };
-        const float maxDist = kBallRadius + len(solverHalf);
-        for (int k = 0; k < d.nCars; k++) {
-            const int c = base + k;
-            if (d.ci(CARL_CAR_DEMOED, c)) continue;
-            if (lensq(bp - d.cv(CARL_CAR_CEN, c)) > maxDist * maxDist) continue;
-            ballCarPair(d, sim, c, preVel, tick);
-        }
-    }
-    const V3 corrected = d.sv(CARL_SIM_BALL_POS, sim);
-    if (lensq(corrected - exported) != 0.f) posBT = corrected * .02f;
-    const V3 finalVel = d.sv(CARL_SIM_BALL_VEL, sim);
-    velBT = lensq(finalVel - preVel) == 0.f ? preBT : finalVel * .02f;
+    for (int k = 0; k < d.nCars; k++)
+        if (near & (1u << k)) ballCarPair(d, sim, base + k, preVel, tick, pos, vel, ang);
+    d.ssetv(CARL_SIM_BALL_VEL, sim, vel);
+    d.ssetv(CARL_SIM_BALL_ANG, sim, ang);
+    if (lensq(pos - exported) != 0.f) posBT = pos * .02f;
+    velBT = lensq(vel - preVel) == 0.f ? preBT : vel * .02f;
     posBT = posBT + (pushVel * .02f) * kDt;
     posBT = posBT + velBT * kDt;
     const V3 ballPos = posBT * 50.f;
@@ -1255,7 +1259,7 @@ DI void ballTickWith(const Dev& d, int sim, int tick, SolveArena solveArena)
     d.ssetv(CARL_SIM_BALL_INT_POS, sim, posBT);
     d.ssetv(CARL_SIM_BALL_INT_VEL, sim, velBT);
     d.ssetv(CARL_SIM_BALL_EXP_POS, sim, ballPos);
-    d.ssetv(CARL_SIM_BALL_EXP_VEL, sim, finalVel);
+    d.ssetv(CARL_SIM_BALL_EXP_VEL, sim, vel);
     d.sseti(CARL_SIM_BALL_INT_VALID, sim, 1);
 
     const float thr = kGoalThresholdY + kBallRadius;
