@@ -1093,8 +1093,9 @@ DI float extraCurve(float s)
 // (CarBall/Solve.cuh:207-243) for a car that is not demolished.  The ball's
 // position and velocities are the caller's registers, updated in place (the
 // caller stores them); every word of the car the pair reads, and the ball's
-// accumulated impulse, is loaded in one batch before any is tested.
-DI void ballCarPair(const Dev& d, int sim, int c, V3 preBallVel, int tick, V3& ballNow, V3& bv, V3& ba)
+// accumulated impulse, is loaded in one batch before any is tested.  True
+// when the pair is in contact (the ball's velocities have been solved).
+DI bool ballCarPair(const Dev& d, int sim, int c, V3 preBallVel, int tick, V3& ballNow, V3& bv, V3& ba)
 {
     const V3 carPos = d.cv(CARL_CAR_POS, c), carCen = d.cv(CARL_CAR_CEN, c);
     V3 cv = d.cv(CARL_CAR_VEL, c), ca = d.cv(CARL_CAR_ANG, c);
@@ -1114,7 +1115,7 @@ DI void ballCarPair(const Dev& d, int sim, int c, V3 preBallVel, int tick, V3& b
     V3 point, normal;
     float depth;
     if (dsq > 1e-8f) {
-        if (dsq >= accept * accept) return;
+        if (dsq >= accept * accept) return false;
         const float dist = sqrtf(dsq);
         const V3 ln = dl * (1.f / dist);
         point = carCen + rotate(rot, cl + ln * kCarMargin);
@@ -1173,7 +1174,7 @@ DI void ballCarPair(const Dev& d, int sim, int c, V3 preBallVel, int tick, V3& b
 
     d.seti(CARL_CAR_BALL_CONTACT_TICK, c, tick);
     d.sseti(CARL_SIM_LAST_TOUCH_TICK, sim, tick);
-    if (tick <= last + 1 && last <= tick) return;
+    if (tick <= last + 1 && last <= tick) return true;
     d.seti(CARL_CAR_BALL_HIT_TICK, c, tick);
     const V3 relVel = preBallVel - preCarVel;
     const float speed = fmin_(sqrtf(lensq(relVel)), kExtraMaxDv);
@@ -1192,6 +1193,7 @@ DI void ballCarPair(const Dev& d, int sim, int c, V3 preBallVel, int tick, V3& b
         }
     }
     d.ssetv(CARL_SIM_BALL_IMP, sim, ballImp + added);
+    return true;
 }
 
 // drag, arena solve, car contacts, integration in Bullet units and goal check
@@ -1246,10 +1248,13 @@ DI void ballTickWith(const Dev& d, int sim, int tick, SolveArena solveArena)
         ang = b.ang;
         pushVel = b.pushVel;
     }
+    bool moved = !sleeping;
     for (int k = 0; k < d.nCars; k++)
-        if (near & (1u << k)) ballCarPair(d, sim, base + k, preVel, tick, pos, vel, ang);
-    d.ssetv(CARL_SIM_BALL_VEL, sim, vel);
-    d.ssetv(CARL_SIM_BALL_ANG, sim, ang);
+        if (near & (1u << k)) moved |= ballCarPair(d, sim, base + k, preVel, tick, pos, vel, ang);
+    if (moved) {
+        d.ssetv(CARL_SIM_BALL_VEL, sim, vel);
+        d.ssetv(CARL_SIM_BALL_ANG, sim, ang);
+    }
     if (lensq(pos - exported) != 0.f) posBT = pos * .02f;
     velBT = lensq(vel - preVel) == 0.f ? preBT : vel * .02f;
     posBT = posBT + (pushVel * .02f) * kDt;
