@@ -134,6 +134,35 @@ DI bool rayBox(V3 start, V3 dir, V3 center, Q4 rot, float maxDist, float& dist, 
 
 // rays against the other cars of the simulation, then the ball (after the
 // arena, so only strictly nearer hits replace an arena hit)
+// the wheel rays against one other car's box
+DI void raycastCar(const V3* start, V3 dir, V3 ocen, Q4 orot, Wheels& w)
+{
+#pragma unroll
+    for (int k = 0; k < kWheels; k++) {
+        float dd;
+        V3 n;
+        if (!rayBox(start[k], dir, ocen, orot, wheelRay(k), dd, n) || dd >= w.dist[k]) continue;
+        w.dist[k] = dd;
+        w.normal[k] = n;
+        w.src[k] = kSrcCar;
+    }
+}
+
+// the wheel rays against the ball
+DI void raycastBall(const V3* start, V3 dir, V3 ball, Wheels& w)
+{
+    const float invR = 1.f / kBallRadius;
+#pragma unroll
+    for (int k = 0; k < kWheels; k++) {
+        float dd;
+        if (!raySphere(start[k], dir, ball, kBallRadius, wheelRay(k), dd) || dd >= w.dist[k]) continue;
+        w.dist[k] = dd;
+        w.normal[k] = ((start[k] + dir * dd) - ball) * invR;
+        w.src[k] = kSrcBall;
+    }
+}
+
+// the wheel rays against the simulation's other cars, in car order, then the ball
 DI void raycastBodies(const Dev& d, int car, int sim, const V3* start, V3 dir, Wheels& w)
 {
     const int base = sim * d.nCars;
@@ -146,25 +175,9 @@ DI void raycastBodies(const Dev& d, int car, int sim, const V3* start, V3 dir, W
         const V3 ocen = d.cv(CARL_CAR_CEN, oc);
         const Q4 orot = d.cq(CARL_CAR_ROT, oc);
         if (oc == car || demoed) continue;
-#pragma unroll
-        for (int k = 0; k < kWheels; k++) {
-            float dd;
-            V3 n;
-            if (!rayBox(start[k], dir, ocen, orot, wheelRay(k), dd, n) || dd >= w.dist[k]) continue;
-            w.dist[k] = dd;
-            w.normal[k] = n;
-            w.src[k] = kSrcCar;
-        }
+        raycastCar(start, dir, ocen, orot, w);
     }
-    const float invR = 1.f / kBallRadius;
-#pragma unroll
-    for (int k = 0; k < kWheels; k++) {
-        float dd;
-        if (!raySphere(start[k], dir, ball, kBallRadius, wheelRay(k), dd) || dd >= w.dist[k]) continue;
-        w.dist[k] = dd;
-        w.normal[k] = ((start[k] + dir * dd) - ball) * invR;
-        w.src[k] = kSrcBall;
-    }
+    raycastBall(start, dir, ball, w);
 }
 
 DI void storeWheelOutputs(const Dev& d, int car, const Wheels& w)
@@ -1267,9 +1280,10 @@ DI void contactPrepare(ContactLdsT<Owners>& L, int lane, bool sat, V3 cen, Q4 ro
 }
 
 // Owner side, after the search: wheel hits (arena winner, then cars and the
-// ball) and the cell reference of the deepest arena contact (-1 for none).
-template <int Owners>
-DI int contactFinish(const Dev& d, const ContactLdsT<Owners>& L, int lane, int car, int sim, V3 cen, Q4 rot, Wheels& w)
+// ball: bodies(start, dir, w) casts the rays at those) and the cell
+// reference of the deepest arena contact (-1 for none).
+template <int Owners, class Bodies>
+DI int contactFinishWith(const ContactLdsT<Owners>& L, int lane, V3 cen, Q4 rot, Wheels& w, Bodies bodies)
 {
     const V3 up = rotate(rot, kZ);
     const V3 dir = -up;
@@ -1286,9 +1300,16 @@ DI int contactFinish(const Dev& d, const ContactLdsT<Owners>& L, int lane, int c
         w.src[k] = kSrcArena;
         w.normal[k] = V3{ L.rayNrm[k][0][lane], L.rayNrm[k][1][lane], L.rayNrm[k][2][lane] };
     }
-    raycastBodies(d, car, sim, start, dir, w);
+    bodies(start, dir, w);
     const unsigned long long best = L.bestKey[lane];
     return best == kNoKey ? -1 : L.first[lane] + (int)(uint32_t)best;
+}
+
+template <int Owners>
+DI int contactFinish(const Dev& d, const ContactLdsT<Owners>& L, int lane, int car, int sim, V3 cen, Q4 rot, Wheels& w)
+{
+    return contactFinishWith(L, lane, cen, rot, w,
+                             [&](const V3* start, V3 dir, Wheels& ww) { raycastBodies(d, car, sim, start, dir, ww); });
 }
 
 // --------------------------------------------------------------- solver body

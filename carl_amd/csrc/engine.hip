@@ -143,11 +143,13 @@ DI void contactGroup(const Dev& d, const Handoff& out, int screen, int car0, int
     Broad bp{ 0, 0, 0 };
     bool demoed = false, fine = false;
     int first = 0, count = 0;
+    V3 ball = kZero;
     if (ok) {
         cen = d.cv(CARL_CAR_CEN, car);
         rot = d.cq(CARL_CAR_ROT, car);
         bp = broadphase(d, d.cv(CARL_CAR_POS, car), d.cv(CARL_CAR_VEL, car), d.cv(CARL_CAR_ANG, car), cen, rot);
         demoed = d.ci(CARL_CAR_DEMOED, car) != 0;
+        if (d.nCars == 2) ball = d.sv(CARL_SIM_BALL_POS, car >> 1);
         // the shorter of two lists that both hold every triangle the car can
         // touch, in ascending triangle order: the candidate-grid list of the
         // cell holding the car's centre (every triangle within ball reach +
@@ -170,11 +172,30 @@ DI void contactGroup(const Dev& d, const Handoff& out, int screen, int car0, int
         [&](const RefBox& b, int o, int q, int) { contactScreen(L, b, o, q, lane); },
         [&](bool last) { contactDrain(d, L, lane, last); });
     waveSync();
+    // 1v1: the other car of an owner's simulation is the neighbouring lane's
+    // owner (owner groups start at even cars and end at even ones), so its
+    // pre-tick box and flag come from that lane's registers, and the ball's
+    // position was loaded with the owner's own words: the wheel rays at the
+    // bodies wait for no load
+    V3 ocen = kZero;
+    Q4 orot{ 0.f, 0.f, 0.f, 1.f };
+    bool odemoed = true;
+    if (d.nCars == 2) {
+        ocen = V3{ __shfl_xor(cen.x, 1), __shfl_xor(cen.y, 1), __shfl_xor(cen.z, 1) };
+        orot = Q4{ __shfl_xor(rot.x, 1), __shfl_xor(rot.y, 1), __shfl_xor(rot.z, 1), __shfl_xor(rot.w, 1) };
+        odemoed = __shfl_xor((int)demoed, 1) != 0;
+    }
     Wheels w;
     int best = -1;
     float pt[10] = {};
     if (ok) {
-        best = contactFinish(d, L, lane, car, car / d.nCars, cen, rot, w);
+        if (d.nCars == 2)
+            best = contactFinishWith(L, lane, cen, rot, w, [&](const V3* start, V3 dir, Wheels& ww) {
+                if (!odemoed) raycastCar(start, dir, ocen, orot, ww);
+                raycastBall(start, dir, ball, ww);
+            });
+        else
+            best = contactFinish(d, L, lane, car, car / d.nCars, cen, rot, w);
         if (best >= 0) {
 #pragma unroll
             for (int i = 0; i < 10; i++) pt[i] = L.bestPt[i][lane];
