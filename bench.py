@@ -126,34 +126,50 @@ def summarize_rocprof(trace_dir: str | None, fetch_dir: str | None, write_dir: s
                       copy_fetch_dir: str | None, copy_write_dir: str | None, copy_mib: int,
                       steps: int, warmup: int) -> None:
     """Markdown summary of rocprofv3 output of one bench run: per kernel, the
-    average dispatch duration over all dispatches and over the timed window
-    (dispatches warmup .. warmup+steps-1 of that kernel, in dispatch order;
-    for the packing kernel also the `steps` dispatches after it, over which
-    the bench times it), and the copy-calibrated FETCH_SIZE / WRITE_SIZE
-    bytes per dispatch over the same windows."""
+    average dispatch duration over all dispatches, over the timed env steps
+    (warmup .. warmup+steps-1) and over the `steps` steps after them (over
+    which the bench times the packing kernel), and the copy-calibrated
+    FETCH_SIZE / WRITE_SIZE bytes per dispatch over the same windows.  Every
+    env step ends with one packing-kernel dispatch, so a window is the range
+    of dispatch ids between two of those: a kernel counts in the window its
+    dispatches fall into (set-up dispatches fall into none)."""
     def short(name: str) -> str:
         # "(anonymous namespace)::tickWindowKernel(carl::Dev, ...)" -> "tickWindowKernel"
         head = name.replace("(anonymous namespace)::", "")
         return head.split("(")[0].split("<")[0].split()[-1] if "(" in head else head
 
     def kernel_series(rows, value):
+        # kernel -> [(dispatch id, value)] in dispatch order
         out: dict[str, list] = {}
         for r in sorted(rows, key=lambda r: int(r["Dispatch_Id"])):
-            out.setdefault(short(r["Kernel_Name"]), []).append(value(r))
+            out.setdefault(short(r["Kernel_Name"]), []).append((int(r["Dispatch_Id"]), value(r)))
         return out
+
+    def step_windows(series):
+        # dispatch-id ranges (lo, hi] of the timed steps and of the steps after
+        ends = [i for i, _ in series.get(PACK_KERNEL, [])]
+
+        def end(step):
+            return -1 if step < 0 or not ends else ends[min(step, len(ends) - 1)]
+        return {"timed": (end(warmup - 1), end(warmup + steps - 1)),
+                "after": (end(warmup + steps - 1), end(warmup + 2 * steps - 1))}
+
+    def pick(xs, window):
+        lo, hi = window
+        return [v for i, v in xs if lo < i <= hi]
 
     def mean(xs):
         return sum(xs) / len(xs) if xs else float("nan")
 
-    windows = {"timed": (warmup, warmup + steps), "after": (warmup + steps, warmup + 2 * steps)}
     if trace_dir:
         rows = _read_csv(next(Path(trace_dir).rglob("*kernel_trace.csv")))
         dur = kernel_series(rows, lambda r: (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+        windows = step_windows(dur)
         print("| kernel | dispatches | avg us (all) | avg us (timed steps) | avg us (steps after) |")
         print("|---|---|---|---|---|")
-        for k, xs in sorted(dur.items(), key=lambda kv: -sum(kv[1])):
-            w = {n: mean(xs[a:b]) for n, (a, b) in windows.items()}
-            print(f"| {k} | {len(xs)} | {mean(xs):.1f} | {w['timed']:.1f} | {w['after']:.1f} |")
+        for k, xs in sorted(dur.items(), key=lambda kv: -sum(v for _, v in kv[1])):
+            w = {n: mean(pick(xs, win)) for n, win in windows.items()}
+            print(f"| {k} | {len(xs)} | {mean([v for _, v in xs]):.1f} | {w['timed']:.1f} | {w['after']:.1f} |")
         print()
 
     def counter(dir_, name):
@@ -162,19 +178,20 @@ def summarize_rocprof(trace_dir: str | None, fetch_dir: str | None, write_dir: s
 
     if fetch_dir and write_dir and copy_fetch_dir and copy_write_dir:
         copy_bytes = copy_mib * (1 << 20)
-        cf = max(mean(v) for v in counter(copy_fetch_dir, "FETCH_SIZE").values())
-        cw = max(mean(v) for v in counter(copy_write_dir, "WRITE_SIZE").values())
+        cf = max(mean([x for _, x in v]) for v in counter(copy_fetch_dir, "FETCH_SIZE").values())
+        cw = max(mean([x for _, x in v]) for v in counter(copy_write_dir, "WRITE_SIZE").values())
         f_scale, w_scale = copy_bytes / (cf * 1024), copy_bytes / (cw * 1024)
         print(f"Calibration: a {copy_mib} MiB device copy reads FETCH_SIZE {cf:.1f} KiB and WRITE_SIZE {cw:.1f} KiB: "
               f"FETCH_SIZE x {f_scale:.3f}, WRITE_SIZE x {w_scale:.3f} to bytes.")
         print()
         fetch, write = counter(fetch_dir, "FETCH_SIZE"), counter(write_dir, "WRITE_SIZE")
+        fwin, wwin = step_windows(fetch), step_windows(write)
         print("| kernel | window | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | HBM bytes (scaled) |")
         print("|---|---|---|---|---|---|")
         lines = []
-        for k in sorted(fetch, key=lambda k: -sum(fetch[k])):
-            for n, (a, b) in windows.items():
-                fk, wk = fetch[k][a:b], write.get(k, [])[a:b]
+        for k in sorted(fetch, key=lambda k: -sum(v for _, v in fetch[k])):
+            for n in fwin:
+                fk, wk = pick(fetch[k], fwin[n]), pick(write.get(k, []), wwin[n])
                 if not fk or not wk:
                     continue
                 total = mean(fk) * 1024 * f_scale + mean(wk) * 1024 * w_scale

@@ -32,3 +32,46 @@ def test_table_layout():
     # 65536 simulations per tick in 40 us
     assert lines[12] == "sim ticks/s       1638.4M"
     assert len(lines) == 13
+
+
+def test_rocprof_summary_windows_follow_the_steps(tmp_path, capsys):
+    """bench.py's rocprof summary: set-up dispatches count in no window, and
+    each kernel's timed and after windows are the dispatches between the
+    packing-kernel dispatches that end env steps warmup-1, warmup+steps-1 and
+    warmup+2*steps-1 (durations chosen so that each window has its own mean)."""
+    import csv
+    import sys
+    from pathlib import Path
+
+    sys.path.insert(0, str(Path(__file__).resolve().parent.parent))
+    import bench
+
+    warmup, steps, total = 2, 3, 10
+    rows, t = [], 0
+
+    def add(name, us):
+        nonlocal t
+        rows.append({"Dispatch_Id": len(rows) + 1, "Kernel_Name": name,
+                     "Start_Timestamp": t, "End_Timestamp": t + int(us * 1000)})
+        t += 10**6
+
+    for _ in range(4):
+        add("__amd_rocclr_fillBufferAligned", 50.0)
+    for step in range(total):
+        window = 1 if warmup <= step < warmup + steps else 2 if warmup + steps <= step < warmup + 2 * steps else 0
+        add("(anonymous namespace)::tickWindowKernel(carl::Dev, int)", 100.0 * (window + 1))
+        add("(anonymous namespace)::stepEnvKernel(carl::Dev, carl::StepIO)", 10.0 * (window + 1))
+        add("at::native::reward", 1.0)
+    trace = tmp_path / "trace"
+    trace.mkdir()
+    with open(trace / "run_kernel_trace.csv", "w", newline="") as fh:
+        w = csv.DictWriter(fh, fieldnames=list(rows[0]))
+        w.writeheader()
+        w.writerows(rows)
+    bench.summarize_rocprof(str(trace), None, None, None, None, 512, steps, warmup)
+    table = {line.split(" | ")[0].strip("| "): line.split(" | ")[1:]
+             for line in capsys.readouterr().out.splitlines() if line.startswith("| ") and "---" not in line}
+    assert table["tickWindowKernel"] == ["10", "190.0", "200.0", "300.0 |"]
+    assert table["stepEnvKernel"] == ["10", "19.0", "20.0", "30.0 |"]
+    assert table["__amd_rocclr_fillBufferAligned"] == ["4", "50.0", "nan", "nan |"]
+    assert table["at::native::reward"][2:] == ["1.0", "1.0 |"]
