@@ -95,24 +95,30 @@ def packing_bytes(n_cars: int, obs_dim: int, state_dim: int) -> int:
     return writes + reads
 
 
-TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_1v1_n65536_ts8.md"
+# committed rocprofv3 FETCH_SIZE / WRITE_SIZE summaries of the headline
+# workload: the 20-step bench and the 1,000-step default
+TRAFFIC_FILES = (ROOT / "profiles" / "hbm_traffic_1v1_n65536_ts8.md",
+                 ROOT / "profiles" / "hbm_traffic_1v1_n65536_ts8_steps1000.md")
 
 
 def measured_traffic(kernel: str, n_sim: int, n_cars: int, tick_skip: int, parts: int, window: int,
                      steps: int, warmup: int, tag: str = "traffic"):
-    """HBM bytes per dispatch of `kernel` from the committed rocprofv3
-    FETCH_SIZE / WRITE_SIZE summary of the headline workload (copy-calibrated),
-    for the same window of steps (`steps` timed after `warmup`; tag
-    "traffic-after" for the `steps` steps after them, over which the packing
-    kernel is timed); None for any other workload or window, or when the
-    summary is absent."""
-    if (n_sim, n_cars, tick_skip, parts, window) != (65536, 2, 8, 1, 64) or not TRAFFIC_FILE.is_file():
-        return None
-    for line in TRAFFIC_FILE.read_text().splitlines():
-        f = line.split()
-        if len(f) == 5 and f[0] == tag and f[1] == kernel and (int(f[2]), int(f[3])) == (steps, warmup):
-            return int(f[4])
-    return None
+    """(HBM bytes per dispatch of `kernel`, summary file name) from the
+    committed rocprofv3 FETCH_SIZE / WRITE_SIZE summaries of the headline
+    workload (copy-calibrated), for the same window of steps (`steps` timed
+    after `warmup`; tag "traffic-after" for the steps after them, at most
+    200, over which the packing kernel is timed); (None, None) for any other
+    workload, launch shape or window, or when no summary holds it."""
+    if (n_sim, n_cars, tick_skip, parts, window) != (65536, 2, 8, 1, 64):
+        return None, None
+    for path in TRAFFIC_FILES:
+        if not path.is_file():
+            continue
+        for line in path.read_text().splitlines():
+            f = line.split()
+            if len(f) == 5 and f[0] == tag and f[1] == kernel and (int(f[2]), int(f[3])) == (steps, warmup):
+                return int(f[4]), path.name
+    return None, None
 
 
 def _read_csv(path: Path) -> list[dict]:
@@ -361,6 +367,8 @@ def main() -> None:
     launch_bytes = kernel_bytes(kernel, n_cars, args.tick_skip) * launch_sims
     achieved = launch_bytes / (launch_ms * 1e-3) / 1e9
     tick_ms = sum(ms for ms, _ in timing.values())
+    traffic, traffic_source = measured_traffic(kernel, n_sim, n_cars, args.tick_skip, parts,
+                                               env.tick_window_launch, args.steps, args.warmup)
 
     result = {
         "metric": METRIC,
@@ -385,7 +393,7 @@ def main() -> None:
             "tick_skip": args.tick_skip,
             "parallelism": "single GPU",
             "tick_streams": parts,
-            "tick_window": env.tick_window,
+            "tick_window": env.tick_window_launch,
             "timed_steps": f"env steps {args.warmup + 1}..{args.warmup + args.steps} after the initial reset",
         },
         "roofline": {
@@ -395,9 +403,8 @@ def main() -> None:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": measured_traffic(kernel, n_sim, n_cars, args.tick_skip, parts, env.tick_window,
-                                        args.steps, args.warmup),
-            "traffic_source": TRAFFIC_FILE.name,
+            "traffic": traffic,
+            "traffic_source": traffic_source,
             "launch_ms": launch_ms,
             "launches": launches,
             "bytes_per_launch": launch_bytes,
@@ -425,9 +432,8 @@ def main() -> None:
             "launch_ms": pack_ms,
             "launches": pack_timing[1],
             "bytes_per_launch": pack_bytes,
-            "traffic": measured_traffic(PACK_KERNEL, n_sim, n_cars, args.tick_skip, parts, env.tick_window,
-                                        args.steps, args.warmup, tag="traffic-after")
-            if args.steps <= 200 else None,
+            "traffic": measured_traffic(PACK_KERNEL, n_sim, n_cars, args.tick_skip, parts,
+                                        env.tick_window_launch, args.steps, args.warmup, tag="traffic-after")[0],
         }
     if stages is not None:
         result["stage_profile"] = stages

@@ -234,7 +234,8 @@ std::string buildArena(const std::string& objPath, HostArena& out)
     // bounds that screen nothing.
     float vmaxAbs = 0.f;
     for (const V3& v : verts) vmaxAbs = std::max(vmaxAbs, std::max(std::fabs(v.x), std::max(std::fabs(v.y), std::fabs(v.z))));
-    std::vector<float> screen(16 * (size_t)nTris);
+    std::vector<float>& screen = out.triBoxes;
+    screen.assign(16 * (size_t)nTris, 0.f);
     const double eps = std::ldexp(1.0, -24), g = 16.0 * eps, T = 32768.0, L = 64.0, grow = 1.25;
     for (int t = 0; t < nTris; t++) {
         const float* rec = &out.triRecords[16 * (size_t)t];
@@ -296,7 +297,8 @@ std::string buildArena(const std::string& objPath, HostArena& out)
         const size_t nFine = (size_t)out.fineStart[kFineCells];
         out.fineRecords.assign(16 * nFine, 0.f);
         out.fineAux.assign(4 * nFine, 0.f);
-        out.fineBoxes.assign(16 * nFine, 0.f);
+        out.fineTris.assign(nFine, 0);
+        out.triAux.assign(4 * (size_t)nTris, 0.f);
         std::fill(fcount.begin(), fcount.end(), 0);
         for (int t = 0; t < nTris; t++) {
             int a[3], b[3];
@@ -304,26 +306,21 @@ std::string buildArena(const std::string& objPath, HostArena& out)
             const auto& r = range[t];
             const uint32_t reg = (uint32_t)r[0] | (uint32_t)r[3] << 6 | (uint32_t)r[1] << 12 | (uint32_t)r[4] << 18 |
                                  (uint32_t)r[2] << 24 | (uint32_t)r[5] << 28;
+            std::memcpy(&out.triAux[4 * (size_t)t], &out.angles[3 * (size_t)t], 3 * sizeof(float));
+            std::memcpy(&out.triAux[4 * (size_t)t + 3], &reg, sizeof reg);
             for (int z = a[2]; z <= b[2]; z++)
                 for (int y = a[1]; y <= b[1]; y++)
                     for (int x = a[0]; x <= b[0]; x++) {
                         const int c = x + kFineX * (y + kFineY * z);
                         const size_t f = (size_t)out.fineStart[c] + fcount[c]++;
                         std::memcpy(&out.fineRecords[16 * f], &out.triRecords[16 * (size_t)t], 16 * sizeof(float));
-                        std::memcpy(&out.fineBoxes[16 * f], &screen[16 * (size_t)t], 16 * sizeof(float));
-                        std::memcpy(&out.fineAux[4 * f], &out.angles[3 * (size_t)t], 3 * sizeof(float));
-                        std::memcpy(&out.fineAux[4 * f + 3], &reg, sizeof reg);
+                        std::memcpy(&out.fineAux[4 * f], &out.triAux[4 * (size_t)t], 4 * sizeof(float));
+                        out.fineTris[f] = t;
                     }
         }
     }
-    out.refBoxes.assign(16 * (size_t)nRefs, 0.f);
-    out.refAngles.assign(4 * (size_t)nRefs, 0.f);
-    for (int r = 0; r < nRefs; r++) {
-        const int t = out.cellTris[r];
-        std::memcpy(&out.refAngles[4 * (size_t)r], &out.angles[3 * (size_t)t], 3 * sizeof(float));
-        std::memcpy(&out.records[16 * (size_t)r], &out.triRecords[16 * (size_t)t], 16 * sizeof(float));
-        std::memcpy(&out.refBoxes[16 * (size_t)r], &screen[16 * (size_t)t], 16 * sizeof(float));
-    }
+    for (int r = 0; r < nRefs; r++)
+        std::memcpy(&out.records[16 * (size_t)r], &out.triRecords[16 * (size_t)out.cellTris[r]], 16 * sizeof(float));
     return "";
 }
 

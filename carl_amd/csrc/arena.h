@@ -16,12 +16,12 @@ struct HostArena {
     std::vector<int> cellTris;      // triangle per cell reference, ascending within a cell
     std::vector<float> records;     // 16 floats per cell reference (device layout, see state.h)
     std::vector<float> triRecords;  // the same 16 floats per triangle, by triangle index
-    std::vector<float> refBoxes;    // 16 floats per cell reference: contact-search screening data
-    std::vector<float> refAngles;   // 4 per cell reference: the triangle's signed edge angles xyz, 0
+    std::vector<float> triBoxes;    // 16 floats per triangle: contact-search screening data
+    std::vector<float> triAux;      // 4 per triangle: edge angles xyz, registration range (bits)
     std::vector<int> fineStart;     // kFineCells + 1 offsets into fineRecords (in references)
     std::vector<float> fineRecords; // 16 floats per ball-grid reference (record layout), ascending per cell
     std::vector<float> fineAux;     // 4 per ball-grid reference: edge angles xyz, registration range (bits)
-    std::vector<float> fineBoxes;   // 16 floats per ball-grid reference: contact-search screening data
+    std::vector<int> fineTris;      // triangle per ball-grid reference, ascending within a cell
     // native mesh metadata (only with CARL_ARENA_METADATA), 16 floats per
     // triangle: native vertex 0 xyz, order key (int bits, mesh * 10000 +
     // order); vertex 1 xyz, native mesh (int bits); vertex 2 xyz, edge flags

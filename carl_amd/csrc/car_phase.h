@@ -1004,7 +1004,7 @@ struct ContactLdsT {
     float rayNrm[kWheels][3][Owners];   // surface normal of each wheel's nearest arena hit
     float bestPt[10][Owners];           // manifold point of the deepest arena contact so far
     // screened items in run order, entries owner << 24 | kQueueSat (the SAT
-    // may accept it) | item
+    // may accept it) | triangle
     int candQ[128];
     int candN;
 };
@@ -1029,6 +1029,7 @@ DI V3 ownerDir(const ContactLdsT<Owners>& L, int o)
 struct RefBox {
     float4 lo, hi, pl, sat;
     bool live;   // an item of the owner's broadphase cell
+    int tri;     // the triangle
 };
 
 // Whether a triangle with packed registration range `reg` (x0 x1 y0 y1 6 bits
@@ -1040,19 +1041,34 @@ DI bool registeredIn(uint32_t reg, int bcell)
            y <= (int)((reg >> 18) & 63) && (int)((reg >> 24) & 15) <= z && z <= (int)(reg >> 28);
 }
 
-// screening data of item q of owner o (reference 0 for lanes without an
-// item).  An item of a candidate-grid run counts only when the triangle is
-// listed in the owner's broadphase cell: the reference tests exactly the
-// triangles of that cell.
+// The triangle of item q of owner o's run: an entry of a candidate-grid list
+// or of a broadphase cell's run (both in ascending triangle order).
+template <int Owners>
+DI int contactIndex(const Dev& d, const ContactLdsT<Owners>& L, int o, int q, bool valid)
+{
+    const int ref = valid ? L.first[o] + q : 0;
+    return (L.fine[o] ? d.arena.fineTri : d.arena.cellTri)[ref];
+}
+
+// The screening data of triangle `tri` for owner o, from the per-triangle
+// tables (triangle 0 for lanes without an item).  An item of a candidate-grid
+// run counts only when the triangle is listed in the owner's broadphase cell:
+// the reference tests exactly the triangles of that cell.
+template <int Owners>
+DI RefBox contactFetchTri(const Dev& d, const ContactLdsT<Owners>& L, int tri, int o, bool valid)
+{
+    const int t = valid ? tri : 0;
+    const float4* b = d.arena.triBox + 4 * (size_t)t;
+    bool live = valid;
+    if (L.fine[o]) live = live && registeredIn(__float_as_uint(d.arena.triAux[t].w), L.bcell[o]);
+    return RefBox{ b[0], b[1], b[2], b[3], live, t };
+}
+
+// Both in one dependent fetch (paths off the tick's critical path).
 template <int Owners>
 DI RefBox contactFetch(const Dev& d, const ContactLdsT<Owners>& L, int o, int q, bool valid)
 {
-    const int ref = valid ? L.first[o] + q : 0;
-    const bool fine = L.fine[o] != 0;
-    const float4* b = (fine ? d.arena.fineBox : d.arena.box) + 4 * (size_t)ref;
-    bool live = valid;
-    if (fine) live = live && registeredIn(__float_as_uint(d.arena.fineAux[ref].w), L.bcell[o]);
-    return RefBox{ b[0], b[1], b[2], b[3], live };
+    return contactFetchTri(d, L, contactIndex(d, L, o, q, valid), o, valid);
 }
 
 DI void waveSync()
@@ -1071,7 +1087,7 @@ DI bool boxAxisMiss(V3 axis, V3 w, V3 half, float face)
 
 // screen stage: queue the item unless the heavy stage provably rejects it
 template <int Owners>
-DI void contactScreen(ContactLdsT<Owners>& L, const RefBox& b, int o, int q, int lane)
+DI void contactScreen(ContactLdsT<Owners>& L, const RefBox& b, int o, int lane)
 {
     const float4 s0 = L.scr[0][o], s1 = L.scr[1][o], s2 = L.scr[2][o], s3 = L.scr[3][o], s4 = L.scr[4][o];
     const V3 tlo{ b.lo.x, b.lo.y, b.lo.z }, thi{ b.hi.x, b.hi.y, b.hi.z };
@@ -1103,7 +1119,7 @@ DI void contactScreen(ContactLdsT<Owners>& L, const RefBox& b, int o, int q, int
     // bit 23: the SAT may accept the item (the screen could not prove it
     // rejects; only the rays keep the others)
     const int satBit = (s4.z == 0.f || !satMiss) ? kQueueSat : 0;
-    if (keep) L.candQ[n0 + __popcll(m & lanesBelow(lane))] = (o << 24) | satBit | q;
+    if (keep) L.candQ[n0 + __popcll(m & lanesBelow(lane))] = (o << 24) | satBit | b.tri;
     if (lane == (int)__builtin_ctzll(__ballot(1))) L.candN = n0 + __popcll(m);
 }
 
@@ -1111,7 +1127,10 @@ DI void contactScreen(ContactLdsT<Owners>& L, const RefBox& b, int o, int q, int
 // Queue entries are in run order, so one owner's entries in a chunk sit on
 // consecutive lanes.  SAT hits within the owner's first kMaxTriHits generate
 // their contacts here; each wheel's nearest ray hit so far leaves its normal
-// in LDS, so the owner needs no triangle load afterwards.
+// in LDS, so the owner needs no triangle load afterwards.  An owner's run is
+// in ascending triangle order, so its triangle indices order its items as
+// their run positions do: the minima keyed by triangle break ties as a
+// sequential walk of the run keeps its first hit.
 template <int Owners>
 DI void contactHeavy(const Dev& d, ContactLdsT<Owners>& L, int lane)
 {
@@ -1119,19 +1138,17 @@ DI void contactHeavy(const Dev& d, ContactLdsT<Owners>& L, int lane)
     const int take = n < 64 ? n : 64;
     const bool active = lane < take;
     const int e = active ? L.candQ[lane] : 0;
-    const int o = e >> 24, q = e & (kQueueSat - 1);
+    const int o = e >> 24, q = e & (kQueueSat - 1);   // q: the triangle
     const bool satNeeded = (e & kQueueSat) != 0;
     bool rayHit = false;
     V3 fn = kZero;   // surface normal facing against the rays, for lanes with a ray hit
     bool hasContact = false;
     ManPt manPt{};   // this lane's contact as a manifold point
     if (active) {
-        const int ref = L.first[o] + q;
-        const bool fine = L.fine[o] != 0;
-        const Tri t = unpackTri((fine ? d.arena.fineRec : d.arena.rec) + 4 * (size_t)ref);
+        const Tri t = loadTriIdx(d.arena, q);
         // the edge angles a contact's edge adjustment needs, loaded with the
         // triangle (one round trip instead of two)
-        const float4 ang = fine ? d.arena.fineAux[ref] : d.arena.refAng[ref];
+        const float4 ang = d.arena.triAux[q];
         const V3 dir = ownerDir(L, o);
         const V3 pv = cross(dir, t.e2);
         const float det = dot(t.e1, pv);
@@ -1280,8 +1297,8 @@ DI void contactPrepare(ContactLdsT<Owners>& L, int lane, bool sat, V3 cen, Q4 ro
 }
 
 // Owner side, after the search: wheel hits (arena winner, then cars and the
-// ball: bodies(start, dir, w) casts the rays at those) and the cell
-// reference of the deepest arena contact (-1 for none).
+// ball: bodies(start, dir, w) casts the rays at those) and the
+// triangle of the deepest arena contact (-1 for none).
 template <int Owners, class Bodies>
 DI int contactFinishWith(const ContactLdsT<Owners>& L, int lane, V3 cen, Q4 rot, Wheels& w, Bodies bodies)
 {
@@ -1302,7 +1319,7 @@ DI int contactFinishWith(const ContactLdsT<Owners>& L, int lane, V3 cen, Q4 rot,
     }
     bodies(start, dir, w);
     const unsigned long long best = L.bestKey[lane];
-    return best == kNoKey ? -1 : L.first[lane] + (int)(uint32_t)best;
+    return best == kNoKey ? -1 : (int)(uint32_t)best;
 }
 
 template <int Owners>

@@ -16,11 +16,14 @@
 // the deepest arena contact).
 #include <dlfcn.h>
 #include <hip/hip_ext.h>
+#include <sys/stat.h>
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
 #include <array>
+#include <climits>
 #include <cstring>
+#include <memory>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -62,8 +65,8 @@ constexpr int kMaxTickStreams = 4;
 
 // Per-tick car workspace between the contact and the car-arena kernels, 31
 // 32-bit words per car: wheel hit distance, normal xyz and source per wheel,
-// then the cell reference of the deepest arena contact.
-// kWsBest: cell reference of the deepest arena contact (-1: none); kWsMan:
+// then the triangle of the deepest arena contact.
+// kWsBest: triangle of the deepest arena contact (-1: none); kWsMan:
 // that contact as a manifold point (car-local point xyz, world point xyz,
 // world normal xyz, signed distance)
 enum : int { kWsDist = 0, kWsNx = 4, kWsNy = 8, kWsNz = 12, kWsSrc = 16, kWsBest = 20, kWsMan = 21, kWsPlanes = 31 };
@@ -131,8 +134,10 @@ static_assert(sq(kBackX) + sq(kBackY) + sq(kBackRay + 1.f) < sq(kGridReach), "ba
 
 // The contact search of cars [car0, car0 + Owners) (those below
 // carEnd) by one wave; L is that wave's own LDS.  Every lane of the wave calls
-// it; it synchronises the wave only.
-template <int Depth, int Owners, class Handoff>
+// it; it synchronises the wave only.  The candidates' triangle indices are
+// loaded Lead + 1 rounds of 64 items ahead of the screen, their screening
+// data one round ahead.
+template <int Lead, int Owners, class Handoff>
 DI void contactGroup(const Dev& d, const Handoff& out, int screen, int car0, int carEnd, ContactLdsT<Owners>& L,
                      int lane)
 {
@@ -167,9 +172,10 @@ DI void contactGroup(const Dev& d, const Handoff& out, int screen, int car0, int
     }
     contactPrepare(L, lane, ok && !demoed, cen, rot, first, fine, bp.cell, screen != 0);
     waveSync();
-    waveItemsDeep<Depth>(
-        count, L.excl, [&](int o, int q, bool valid) { return contactFetch(d, L, o, q, valid); },
-        [&](const RefBox& b, int o, int q, int) { contactScreen(L, b, o, q, lane); },
+    waveItemsIndexed<Lead>(
+        count, L.excl, [&](int o, int q, bool valid) { return contactIndex(d, L, o, q, valid); },
+        [&](int tri, int o, bool valid) { return contactFetchTri(d, L, tri, o, valid); },
+        [&](const RefBox& b, int o, int) { contactScreen(L, b, o, lane); },
         [&](bool last) { contactDrain(d, L, lane, last); });
     waveSync();
     // 1v1: the other car of an owner's simulation is the neighbouring lane's
@@ -406,11 +412,12 @@ constexpr int kWindowBlock = CARL_WINDOW_BLOCK;
 constexpr int kWindowWaves = kWindowBlock / 64;
 constexpr int kDefaultWindowSims = CARL_WINDOW_SIMS;
 constexpr int kAutoWindowMin = 8;   // smallest automatic window workgroup (simulations)
-// rounds of candidate loads the window kernel's contact search keeps in flight
-#ifndef CARL_WINDOW_CONTACT_DEPTH
-#define CARL_WINDOW_CONTACT_DEPTH 1
+// rounds of candidate-index loads the window kernel's contact search keeps in
+// flight beyond the round of screening-data loads
+#ifndef CARL_WINDOW_CONTACT_LEAD
+#define CARL_WINDOW_CONTACT_LEAD 1
 #endif
-constexpr int kWindowContactDepth = CARL_WINDOW_CONTACT_DEPTH;
+constexpr int kWindowContactLead = CARL_WINDOW_CONTACT_LEAD;
 // cars whose contacts one wave of the window kernel searches together
 #ifndef CARL_WINDOW_CONTACT_OWNERS
 #define CARL_WINDOW_CONTACT_OWNERS 64
@@ -492,7 +499,7 @@ DI void tickWindowBody(Dev d0, uint32_t* __restrict__ ws, int screen, int kind, 
     for (int k = 0; k < ticks; k++) {
         const int tick = tick0 + k;
         for (int g = car0 + wave * kWindowContactOwners; g < carEnd; g += kWindowWaves * kWindowContactOwners)
-            contactGroup<kWindowContactDepth, kWindowContactOwners>(d, LdsHandoff{ L.wave[wave].hand }, screen, g,
+            contactGroup<kWindowContactLead, kWindowContactOwners>(d, LdsHandoff{ L.wave[wave].hand }, screen, g,
                                                                      carEnd, L.wave[wave].contact, lane);
         __syncthreads();
         mark(kStageContact);
@@ -597,6 +604,19 @@ __global__ __launch_bounds__(kWindowBlock, 2) void tickWindowProfileKernel(Dev d
                                                                         unsigned long long* __restrict__ prof)
 {
     tickWindowBody<true, false, Cars>(d, ws, screen, kind, actions, tick0, ticks, simsPerBlock, range, prof);
+}
+
+using ProfileKernel = void (*)(Dev, uint32_t*, int, int, const void*, int, int, int, SimRange, unsigned long long*);
+
+// the profiled twin of windowKernelFor's instance for a car count
+ProfileKernel profileKernelFor(int nCars)
+{
+    switch (nCars) {
+    case 2: return tickWindowProfileKernel<2>;
+    case 4: return tickWindowProfileKernel<4>;
+    case 6: return tickWindowProfileKernel<6>;
+    default: return tickWindowProfileKernel<0>;
+    }
 }
 
 __global__ void resetKernel(Dev d, int nOrange)
@@ -939,7 +959,7 @@ __global__ __launch_bounds__(kContactBlock) void refreshKernel(Dev d, Selection 
     __syncthreads();
     waveItemsPipelined(
         bp.count, L.excl, [&](int o, int q, bool valid) { return contactFetch(d, L, o, q, valid); },
-        [&](const RefBox& b, int o, int q, int) { contactScreen(L, b, o, q, lane); },
+        [&](const RefBox& b, int o, int, int) { contactScreen(L, b, o, lane); },
         [&](bool last) { contactDrain(d, L, lane, last); });
     __syncthreads();
     if (car < 0) return;
@@ -1101,6 +1121,156 @@ std::string libraryDir()
     return ".";
 }
 
+// ------------------------------------------------------------ shared arena
+
+// The arena is read-only, so the environments on one device share a single
+// device copy of it, refcounted and freed with the last of them.  The host
+// build is made once per process for each mesh file and metadata file (the
+// reference builds its host mesh once per process in static locals,
+// src/ArenaMesh.cu:17-28, and gives every environment a device copy).  A
+// file is identified by its path, size and modification time, so a file
+// rewritten in place is built again.
+struct DeviceArena {
+    std::string key;
+    int device = 0;
+    int refs = 0;
+    std::vector<void*> blocks;   // the device allocations, freed together
+    ArenaView view{};
+};
+
+std::mutex arenaMutex;
+std::vector<std::pair<std::string, std::shared_ptr<const HostArena>>> hostArenas;
+std::vector<DeviceArena*> deviceArenas;
+
+std::string fileKey(const std::string& path)
+{
+    struct stat st {};
+    if (stat(path.c_str(), &st) != 0) return path + "|absent";
+    return path + "|" + std::to_string((long long)st.st_size) + "|" + std::to_string((long long)st.st_mtim.tv_sec)
+           + "." + std::to_string((long long)st.st_mtim.tv_nsec);
+}
+
+// The host build for `key`, made on first use; a failed build is not kept.
+// Called with arenaMutex held.
+int hostArenaFor(const std::string& key, const std::string& obj, const char* meta,
+                 std::shared_ptr<const HostArena>* out)
+{
+    for (const auto& kv : hostArenas)
+        if (kv.first == key) {
+            *out = kv.second;
+            return CARL_OK;
+        }
+    auto host = std::make_shared<HostArena>();
+    std::string err = buildArena(obj, *host);
+    // the native mesh metadata, when named (src/ArenaMesh.cu:69-99)
+    if (err.empty() && meta) err = readArenaMetadata(meta, *host);
+    if (!err.empty()) return fail(CARL_ERR_ARENA, err);
+    hostArenas.emplace_back(key, host);
+    *out = host;
+    return CARL_OK;
+}
+
+template <typename T, typename S>
+int uploadBlock(DeviceArena* a, const S* src, size_t bytes, const T** dst)
+{
+    void* p = nullptr;
+    HIP_TRY(hipMalloc(&p, std::max<size_t>(bytes, 16)));
+    a->blocks.push_back(p);
+    if (bytes) HIP_TRY(hipMemcpy(p, src, bytes, hipMemcpyHostToDevice));
+    *dst = (const T*)p;
+    return CARL_OK;
+}
+
+void freeDeviceArena(DeviceArena* a)
+{
+    for (void* p : a->blocks) (void)hipFree(p);
+    delete a;
+}
+
+int uploadArena(const HostArena& host, DeviceArena* a)
+{
+    ArenaView& v = a->view;
+    std::vector<float4> ang(host.angles.size() / 3);
+    for (size_t t = 0; t < ang.size(); t++)
+        ang[t] = make_float4(host.angles[3 * t], host.angles[3 * t + 1], host.angles[3 * t + 2], 0.f);
+    auto bytes = [](const auto& vec) { return vec.size() * sizeof(vec[0]); };
+    CARL_TRY(uploadBlock(a, host.records.data(), bytes(host.records), &v.rec));
+    CARL_TRY(uploadBlock(a, host.cellStart.data(), bytes(host.cellStart), &v.cellStart));
+    CARL_TRY(uploadBlock(a, ang.data(), bytes(ang), &v.angles));
+    CARL_TRY(uploadBlock(a, host.triRecords.data(), bytes(host.triRecords), &v.tri));
+    CARL_TRY(uploadBlock(a, host.cellTris.data(), bytes(host.cellTris), &v.cellTri));
+    CARL_TRY(uploadBlock(a, host.triBoxes.data(), bytes(host.triBoxes), &v.triBox));
+    CARL_TRY(uploadBlock(a, host.triAux.data(), bytes(host.triAux), &v.triAux));
+    CARL_TRY(uploadBlock(a, host.fineRecords.data(), bytes(host.fineRecords), &v.fineRec));
+    CARL_TRY(uploadBlock(a, host.fineAux.data(), bytes(host.fineAux), &v.fineAux));
+    CARL_TRY(uploadBlock(a, host.fineTris.data(), bytes(host.fineTris), &v.fineTri));
+    CARL_TRY(uploadBlock(a, host.fineStart.data(), bytes(host.fineStart), &v.fineStart));
+    v.native = nullptr;
+    if (!host.nativeRecords.empty())
+        CARL_TRY(uploadBlock(a, host.nativeRecords.data(), bytes(host.nativeRecords), &v.native));
+    return CARL_OK;
+}
+
+// The arena named by CARL_ARENA_OBJ (else the packaged mesh) and
+// CARL_ARENA_METADATA on the current device, one more reference to it.  The
+// host build and its errors come before any device work.
+int acquireArena(DeviceArena** out)
+{
+    *out = nullptr;
+    const std::string obj = findArenaObj(libraryDir());
+    const char* meta = std::getenv("CARL_ARENA_METADATA");
+    const std::string key = fileKey(obj) + "\n" + (meta ? fileKey(meta) : std::string("-"));
+    std::lock_guard<std::mutex> lock(arenaMutex);
+    std::shared_ptr<const HostArena> host;
+    CARL_TRY(hostArenaFor(key, obj, meta, &host));
+    int device = 0;
+    HIP_TRY(hipGetDevice(&device));
+    for (DeviceArena* a : deviceArenas)
+        if (a->device == device && a->key == key) {
+            a->refs++;
+            *out = a;
+            return CARL_OK;
+        }
+    auto* a = new DeviceArena();
+    a->key = key;
+    a->device = device;
+    const int rc = uploadArena(*host, a);
+    if (rc) {
+        freeDeviceArena(a);
+        return rc == CARL_ERR_RUNTIME ? fail(CARL_ERR_RUNTIME, "arena upload failed: " + g_lastError) : rc;
+    }
+    a->refs = 1;
+    deviceArenas.push_back(a);
+    *out = a;
+    return CARL_OK;
+}
+
+void releaseArena(DeviceArena* a)
+{
+    if (!a) return;
+    std::lock_guard<std::mutex> lock(arenaMutex);
+    if (--a->refs > 0) return;
+    deviceArenas.erase(std::find(deviceArenas.begin(), deviceArenas.end(), a));
+    freeDeviceArena(a);
+}
+
+// The tiled state blocks and the tick workspace are addressed through 32-bit
+// buffer resources (a byte count and a 32-bit byte offset per access), so
+// each must stay below 2^31 bytes: at most kMaxCars cars in all (the car
+// block, 4 * CARL_CAR_FIELDS bytes per car, is the largest of the three).
+constexpr long long kMaxCars = (INT_MAX / (4LL * CARL_CAR_FIELDS)) & ~63LL;
+static_assert(kMaxCars * 4LL * kWsPlanes <= INT_MAX && kMaxCars * 4LL * CARL_SIM_FIELDS <= INT_MAX,
+              "the car block bounds the workspace and the simulation block");
+
+int checkSizes(int nSim, int nCars)
+{
+    const long long cars = (long long)nSim * nCars;
+    if (cars > kMaxCars)
+        return fail(CARL_ERR_VALUE, "n_sim * cars per simulation must be at most " + std::to_string(kMaxCars)
+                                        + " (the state's 32-bit byte offsets); got " + std::to_string(cars));
+    return CARL_OK;
+}
+
 }  // namespace
 
 // ------------------------------------------------------------------- engine
@@ -1115,23 +1285,13 @@ struct carl_env {
     hipStream_t stream = nullptr;
     uint32_t* car = nullptr;
     uint32_t* sim = nullptr;
-    float4* rec = nullptr;
-    int* cellStart = nullptr;
-    float4* angles = nullptr;
-    float4* triRec = nullptr;
-    float4* refBox = nullptr;
-    float4* refAng = nullptr;
-    float4* fineRec = nullptr;
-    float4* fineAux = nullptr;
-    float4* fineBox = nullptr;
-    int* fineStart = nullptr;
+    DeviceArena* arena = nullptr;        // shared with the other environments on the device
     float *obs = nullptr, *tobs = nullptr, *state = nullptr, *tstate = nullptr, *rewards = nullptr;
     bool *dones = nullptr, *overtime = nullptr, *tovertime = nullptr;
     int32_t *score = nullptr, *ticks = nullptr, *tscore = nullptr, *tticks = nullptr;
     int32_t* actions = nullptr;
     float* cactions = nullptr;
     uint32_t* ws = nullptr;  // per-tick car workspace (kWsPlanes planes)
-    float4* nativeRec = nullptr;     // native mesh metadata (CARL_ARENA_METADATA), else null
     float* ballScratch = nullptr;    // with it: kNativeMaxContacts slots of kNativeSlotWords per simulation
     int tickStreams = 1;                 // partitions of the tick, one stream each
     int contactScreen = 1;               // screen (car, triangle) pairs in the contact search
@@ -1169,11 +1329,13 @@ struct carl_env {
     {
         Dev d;
         d.car = car; d.sim = sim; d.nSim = nSim; d.nBlue = nBlue; d.nCars = nCars; d.nTotal = nTotal; d.seed = seed;
-        d.arena = ArenaView{ rec, cellStart, angles, triRec, refBox, refAng, fineRec, fineAux, fineBox, fineStart, nativeRec };
+        d.arena = arena->view;
         d.ballScratch = ballScratch;
         return d;
     }
     DoneRule rule() const { return DoneRule{ maxTicks, overtimeTicks, noTouchTicks }; }
+    // native mesh metadata (CARL_ARENA_METADATA)
+    bool native() const { return arena && arena->view.native; }
     int grid(int n, int block) const { return (n + block - 1) / block; }
 };
 
@@ -1189,12 +1351,13 @@ int devAlloc(T** p, size_t count)
 
 void freeAll(carl_env* e)
 {
-    void* ptrs[] = { e->car, e->sim, e->rec, e->cellStart, e->angles, e->triRec, e->refBox, e->refAng, e->fineRec,
-                     e->fineAux, e->fineBox, e->fineStart, e->obs, e->tobs, e->state, e->tstate, e->rewards, e->dones,
+    void* ptrs[] = { e->car, e->sim, e->obs, e->tobs, e->state, e->tstate, e->rewards, e->dones,
                      e->overtime, e->tovertime, e->score, e->ticks, e->tscore, e->tticks, e->actions, e->cactions,
-                     e->ws, e->prof, e->nativeRec, e->ballScratch };
+                     e->ws, e->prof, e->ballScratch };
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
+    releaseArena(e->arena);
+    e->arena = nullptr;
     for (hipEvent_t ev : e->marks) (void)hipEventDestroy(ev);
     for (int i = 0; i < kMaxTickStreams - 1; i++) {
         if (e->join[i]) (void)hipEventDestroy(e->join[i]);
@@ -1283,6 +1446,28 @@ int launchTick(carl_env* e, bool timed, int kernel, void (*k)(P...), dim3 grid, 
 // windowSims > 0 each partition runs all n ticks in one tick-window launch,
 // otherwise four phase kernels per tick.  Timing events bracket partition
 // 0's launches.
+// Simulations per window workgroup for the next launch: the set size capped
+// at a workgroup's cars; until the caller sets it, halved (down to
+// kAutoWindowMin) while every partition's workgroups together still fit the
+// device's resident window workgroups.
+int effectiveWindowSims(const carl_env* e)
+{
+    if (e->windowSims <= 0) return 0;
+    int wsb = std::min(e->windowSims, kWindowBlock / e->nCars);
+    if (!e->windowAuto) return wsb;
+    const int parts = std::min(e->tickStreams, e->nSim);
+    auto blocks = [&](int sims) {
+        int total = 0;
+        for (int p = 0; p < parts; p++) {
+            const int begin = (int)((int64_t)e->nSim * p / parts), end = (int)((int64_t)e->nSim * (p + 1) / parts);
+            total += e->grid(end - begin, sims);
+        }
+        return total;
+    };
+    while (wsb / 2 >= kAutoWindowMin && blocks(wsb / 2) <= e->windowResident) wsb /= 2;
+    return wsb;
+}
+
 int launchTicks(carl_env* e, int kind, const void* actions, int n)
 {
     if (n <= 0) return CARL_OK;
@@ -1300,10 +1485,7 @@ int launchTicks(carl_env* e, int kind, const void* actions, int n)
         for (int p = 1; p < parts; p++) HIP_TRY(hipStreamWaitEvent(stream[p], e->fork, 0));
     }
     if (e->windowSims > 0) {
-        int wsb = std::min(e->windowSims, kWindowBlock / e->nCars);
-        if (e->windowAuto)
-            while (wsb / 2 >= kAutoWindowMin && e->grid(range[0].end - range[0].begin, wsb / 2) <= e->windowResident)
-                wsb /= 2;
+        const int wsb = effectiveWindowSims(e);
         for (int p = 0; p < parts; p++) {
             const SimRange r = range[p];
             const bool timed = p == 0;
@@ -1313,14 +1495,13 @@ int launchTicks(carl_env* e, int kind, const void* actions, int n)
                 const int slots = std::min(blocks, e->profResident);
                 if (e->profSlots != 0 && e->profSlots != slots) e->profMixed = true;
                 e->profSlots = slots;
-                CARL_MARK(launchTick(e, timed, CARL_KERNEL_WINDOW,
-                                     e->nCars == 2 ? tickWindowProfileKernel<2> : tickWindowProfileKernel<0>,
+                CARL_MARK(launchTick(e, timed, CARL_KERNEL_WINDOW, profileKernelFor(e->nCars),
                                      dim3(blocks),
                                      dim3(kWindowBlock), 0, stream[p], d, e->ws, e->contactScreen, kind, actions,
                                      e->tickCount + 1, n, wsb, r, e->prof));
             } else {
                 CARL_MARK(launchTick(e, timed, CARL_KERNEL_WINDOW,
-                                     e->nativeRec ? tickWindowNativeKernel : windowKernelFor(e->nCars),
+                                     e->native() ? tickWindowNativeKernel : windowKernelFor(e->nCars),
                                      dim3(blocks),
                                      dim3(kWindowBlock), 0, stream[p], d, e->ws, e->contactScreen, kind, actions,
                                      e->tickCount + 1, n, wsb, r));
@@ -1338,7 +1519,7 @@ int launchTicks(carl_env* e, int kind, const void* actions, int n)
                                  dim3(kContactBlock), 0, st, d, e->ws, e->contactScreen, r));
             CARL_MARK(launchTick(e, timed, CARL_KERNEL_CAR_ARENA, carArenaKernel, dim3(e->grid(cars, kTickBlock)),
                                  dim3(kTickBlock), 0, st, d, e->ws, kind, actions, tick, r));
-            CARL_MARK(launchTick(e, timed, CARL_KERNEL_BALL, e->nativeRec ? ballNativeKernel : ballKernel,
+            CARL_MARK(launchTick(e, timed, CARL_KERNEL_BALL, e->native() ? ballNativeKernel : ballKernel,
                                  dim3(e->grid(sims, kBallOwners)),
                                  dim3(kBallBlock), 0, st, d, tick, r));
             CARL_MARK(launchTick(e, timed, CARL_KERNEL_FINISH, finishKernel, dim3(e->grid(sims, spb)),
@@ -1479,17 +1660,14 @@ int carl_env_create(int nSim, int nBlue, int nOrange, int seed, int frameskip, i
     if (nSim < 1) return fail(CARL_ERR_VALUE, "n_sim must be at least 1");
     if (nBlue < 0 || nOrange < 0 || nBlue + nOrange < 1) return fail(CARL_ERR_VALUE, "need at least one car");
     if (nBlue > 4 || nOrange > 4) return fail(CARL_ERR_VALUE, "at most 4 cars per team (kickoff spawns)");
+    CARL_TRY(checkSizes(nSim, nBlue + nOrange));
 
-    carl::HostArena host;
-    const std::string path = findArenaObj(libraryDir());
-    std::string err = buildArena(path, host);
-    // the native mesh metadata, when named (src/ArenaMesh.cu:69-99)
-    if (err.empty()) {
-        if (const char* meta = std::getenv("CARL_ARENA_METADATA")) err = readArenaMetadata(meta, host);
-    }
-    if (!err.empty()) return fail(CARL_ERR_ARENA, err);
+    // the host build and its errors come before any device work
+    DeviceArena* arena = nullptr;
+    CARL_TRY(acquireArena(&arena));
 
     carl_env* e = new carl_env();
+    e->arena = arena;
     e->nSim = nSim; e->nBlue = nBlue; e->nOrange = nOrange; e->nCars = nBlue + nOrange;
     e->nTotal = nSim * e->nCars; e->seed = seed; e->frameskip = frameskip;
     e->invert = (flags & CARL_FLAG_INVERT_ORANGE) != 0;
@@ -1525,16 +1703,6 @@ int carl_env_create(int nSim, int nBlue, int nOrange, int seed, int frameskip, i
     int rc = CARL_OK;
     rc = rc ? rc : devAlloc(&e->car, (size_t)CARL_CAR_FIELDS * tiledItems(e->nTotal));
     rc = rc ? rc : devAlloc(&e->sim, (size_t)CARL_SIM_FIELDS * tiledItems(nSim));
-    rc = rc ? rc : devAlloc(&e->rec, host.records.size() / 4);
-    rc = rc ? rc : devAlloc(&e->cellStart, host.cellStart.size());
-    rc = rc ? rc : devAlloc(&e->angles, host.angles.size() / 3);
-    rc = rc ? rc : devAlloc(&e->triRec, host.triRecords.size() / 4);
-    rc = rc ? rc : devAlloc(&e->refBox, host.refBoxes.size() / 4);
-    rc = rc ? rc : devAlloc(&e->refAng, host.refAngles.size() / 4);
-    rc = rc ? rc : devAlloc(&e->fineRec, host.fineRecords.size() / 4);
-    rc = rc ? rc : devAlloc(&e->fineAux, host.fineAux.size() / 4);
-    rc = rc ? rc : devAlloc(&e->fineBox, host.fineBoxes.size() / 4);
-    rc = rc ? rc : devAlloc(&e->fineStart, host.fineStart.size());
     rc = rc ? rc : devAlloc(&e->obs, nT * e->obsDim);
     rc = rc ? rc : devAlloc(&e->tobs, nT * e->obsDim);
     rc = rc ? rc : devAlloc(&e->state, nS * e->stateDim);
@@ -1550,37 +1718,8 @@ int carl_env_create(int nSim, int nBlue, int nOrange, int seed, int frameskip, i
     rc = rc ? rc : devAlloc(&e->actions, nT * 7);
     rc = rc ? rc : devAlloc(&e->cactions, nT * 7);
     rc = rc ? rc : devAlloc(&e->ws, (size_t)kWsPlanes * tiledItems(e->nTotal));
-    if (!host.nativeRecords.empty()) {
-        rc = rc ? rc : devAlloc(&e->nativeRec, host.nativeRecords.size() / 4);
-        rc = rc ? rc : devAlloc(&e->ballScratch, (size_t)kNativeMaxContacts * kNativeSlotWords * nS);
-        if (!rc && hipMemcpy(e->nativeRec, host.nativeRecords.data(), host.nativeRecords.size() * sizeof(float),
-                             hipMemcpyHostToDevice) != hipSuccess)
-            rc = fail(CARL_ERR_RUNTIME, "hipMemcpy failed");
-    }
+    if (e->native()) rc = rc ? rc : devAlloc(&e->ballScratch, (size_t)kNativeMaxContacts * kNativeSlotWords * nS);
     if (rc) return bail(rc);
-
-    std::vector<float4> ang(host.angles.size() / 3);
-    for (size_t t = 0; t < ang.size(); t++)
-        ang[t] = make_float4(host.angles[3 * t], host.angles[3 * t + 1], host.angles[3 * t + 2], 0.f);
-    if (hipMemcpy(e->rec, host.records.data(), host.records.size() * sizeof(float), hipMemcpyHostToDevice) != hipSuccess
-        || hipMemcpy(e->cellStart, host.cellStart.data(), host.cellStart.size() * sizeof(int), hipMemcpyHostToDevice)
-               != hipSuccess
-        || hipMemcpy(e->angles, ang.data(), ang.size() * sizeof(float4), hipMemcpyHostToDevice) != hipSuccess
-        || hipMemcpy(e->triRec, host.triRecords.data(), host.triRecords.size() * sizeof(float), hipMemcpyHostToDevice)
-               != hipSuccess
-        || hipMemcpy(e->refBox, host.refBoxes.data(), host.refBoxes.size() * sizeof(float), hipMemcpyHostToDevice)
-               != hipSuccess
-        || hipMemcpy(e->refAng, host.refAngles.data(), host.refAngles.size() * sizeof(float), hipMemcpyHostToDevice)
-               != hipSuccess
-        || hipMemcpy(e->fineRec, host.fineRecords.data(), host.fineRecords.size() * sizeof(float),
-                     hipMemcpyHostToDevice) != hipSuccess
-        || hipMemcpy(e->fineBox, host.fineBoxes.data(), host.fineBoxes.size() * sizeof(float), hipMemcpyHostToDevice)
-               != hipSuccess
-        || hipMemcpy(e->fineAux, host.fineAux.data(), host.fineAux.size() * sizeof(float), hipMemcpyHostToDevice)
-               != hipSuccess
-        || hipMemcpy(e->fineStart, host.fineStart.data(), host.fineStart.size() * sizeof(int), hipMemcpyHostToDevice)
-               != hipSuccess)
-        return bail(fail(CARL_ERR_RUNTIME, "arena upload failed"));
 
     rc = fullReset(e);
     if (rc) return bail(rc);
@@ -1811,7 +1950,8 @@ int carl_env_get_param(carl_env* e, int p, int* v)
     case CARL_PARAM_TICK_STREAMS: *v = e->tickStreams; break;
     case CARL_PARAM_CONTACT_SCREEN: *v = e->contactScreen; break;
     case CARL_PARAM_TICK_WINDOW: *v = e->windowSims; break;
-    case CARL_PARAM_NATIVE_ARENA: *v = e->nativeRec != nullptr; break;
+    case CARL_PARAM_TICK_WINDOW_LAUNCH: *v = effectiveWindowSims(e); break;
+    case CARL_PARAM_NATIVE_ARENA: *v = e->native(); break;
     default: return fail(CARL_ERR_VALUE, "unknown parameter");
     }
     return CARL_OK;
@@ -1821,7 +1961,7 @@ int carl_env_enable_timing(carl_env* e, int enable)
 {
     CARL_TRY(checkEnv(e));
     HIP_TRY(hipStreamSynchronize(e->stream));
-    if ((enable & CARL_TIME_STAGES) && e->nativeRec)
+    if ((enable & CARL_TIME_STAGES) && e->native())
         return fail(CARL_ERR_VALUE, "the stage profile does not cover the native arena meshes");
     e->timing = enable & (CARL_TIME_TICKS | CARL_TIME_PACKING | CARL_TIME_STAGES);
     e->timedLaunches = 0;
@@ -1838,8 +1978,7 @@ int carl_env_enable_timing(carl_env* e, int enable)
         HIP_TRY(hipGetDevice(&device));
         HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
         HIP_TRY(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, device));
-        HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &perCu, e->nCars == 2 ? tickWindowProfileKernel<2> : tickWindowProfileKernel<0>, kWindowBlock, 0));
+        HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(&perCu, profileKernelFor(e->nCars), kWindowBlock, 0));
         if (khz <= 0 || perCu <= 0) return fail(CARL_ERR_RUNTIME, "no wall-clock rate or window occupancy");
         e->profResident = perCu * cus;
         e->clockMHz = khz / 1000.0;

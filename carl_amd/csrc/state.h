@@ -30,18 +30,19 @@ namespace carl {
 
 constexpr uint32_t kPlaneFlag = 0x80000000u;  // analytic plane triangle: skipped by the car SAT
 
-constexpr int kMaxArenaTris = 1 << 23;  // contact-search queue entries keep a run position in 23 bits
+constexpr int kMaxArenaTris = 1 << 23;  // contact-search queue entries keep a triangle index in 23 bits
 
 struct ArenaView {
     const float4* rec;       // 4 per cell reference
     const int* cellStart;    // kCells + 1 offsets into rec (in references)
     const float4* angles;    // signed edge angles per triangle (xyz)
     const float4* tri;       // 4 per triangle, by triangle index (same record layout)
-    const float4* box;       // 4 per cell reference: contact-search screening data (arena.cpp)
-    const float4* refAng;    // per cell reference: the triangle's signed edge angles (xyz)
+    const int* cellTri;      // triangle per cell reference, ascending within a cell
+    const float4* triBox;    // 4 per triangle: contact-search screening data (arena.cpp)
+    const float4* triAux;    // per triangle: edge angles xyz, packed broadphase registration range
     const float4* fineRec;   // 4 per ball-grid reference (record layout)
     const float4* fineAux;   // per ball-grid reference: edge angles xyz, packed broadphase registration range
-    const float4* fineBox;   // 4 per ball-grid reference: contact-search screening data (as box)
+    const int* fineTri;      // triangle per ball-grid reference, ascending within a cell
     const int* fineStart;    // kFineCells + 1 offsets into fineRec (in references)
     const float4* native;    // 4 per triangle, native mesh metadata (arena.h); null without it
 };

@@ -150,6 +150,70 @@ __device__ __forceinline__ void waveItemsDeep(int count, int* excl, Fetch&& fetc
     }
 }
 
+// waveItemsPipelined for items reached through an index: index(owner, item,
+// valid) loads an item's index and fetch(index, owner, valid) its data
+// through it.  The index loads run Lead + 1 rounds ahead of process(value,
+// owner, base) and the data loads one round ahead, so a round waits for
+// neither load's full latency (the indices are small lists, the data a small
+// per-index table; both stay in the caches that per-item copies of the data
+// overflow).  Same visiting order, lane placement and after() hook as
+// waveItemsPipelined.
+template <int Lead, typename Index, typename Fetch, typename Process, typename After>
+__device__ __forceinline__ void waveItemsIndexed(int count, int* excl, Index&& index, Fetch&& fetch,
+                                                 Process&& process, After&& after)
+{
+    const int lane = (int)(threadIdx.x & 63);
+    const int incl = waveInclusiveScan(count);
+    const int total = __builtin_amdgcn_readlane(incl, 63);
+    excl[lane] = incl - count;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (total == 0) return;
+    auto locate = [&](int j, int& o, int& q) {
+        o = 0;
+        q = 0;
+        if (j < total) {
+#pragma unroll
+            for (int step = 32; step > 0; step >>= 1)
+                if (excl[o + step] <= j) o += step;
+            q = j - excl[o];
+        }
+    };
+    // slot r of the ring holds the owner and index of round m + 1 while
+    // round m (m = r mod Lead) is processed
+    int ringO[Lead], ringX[Lead];
+    int o0, q0;
+    locate(lane, o0, q0);
+    const int x0 = index(o0, q0, lane < total);
+#pragma unroll
+    for (int r = 0; r < Lead; r++) {
+        int q;
+        locate((r + 1) * 64 + lane, ringO[r], q);
+        ringX[r] = index(ringO[r], q, (r + 1) * 64 + lane < total);
+    }
+    auto cur = fetch(x0, o0, lane < total);
+    int curO = o0;
+    for (int base = 0; base < total;) {
+#pragma unroll
+        for (int r = 0; r < Lead; r++) {
+            if (base < total) {
+                const int nextO = ringO[r];
+                auto next = fetch(ringX[r], nextO, base + 64 + lane < total);
+                const int ja = base + (Lead + 1) * 64 + lane;
+                int q;
+                locate(ja, ringO[r], q);
+                ringX[r] = index(ringO[r], q, ja < total);
+                if (base + lane < total) process(cur, curO, base);
+                after(base + 64 >= total);   // every lane; true after the last round
+                cur = next;
+                curO = nextO;
+                base += 64;
+            }
+        }
+    }
+}
+
 // Without a per-round hook.
 template <typename Fetch, typename Process>
 __device__ __forceinline__ void waveItemsPipelined(int count, int* excl, Fetch&& fetch, Process&& process)

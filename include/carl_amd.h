@@ -127,8 +127,12 @@ enum {
                                       to 8 for runs too small to fill the GPU until it is set); 0: four
                                       phase kernels per tick.  Results are identical; no reference
                                       counterpart */
-    CARL_PARAM_NATIVE_ARENA = 14   /* read-only: 1 when the environment was created with native mesh
+    CARL_PARAM_NATIVE_ARENA = 14,  /* read-only: 1 when the environment was created with native mesh
                                       metadata (the reference's ArenaMesh::hasNativeMetadata) */
+    CARL_PARAM_TICK_WINDOW_LAUNCH = 15 /* read-only: simulations per workgroup the next window launch
+                                          uses (CARL_PARAM_TICK_WINDOW capped at 128 cars, after the
+                                          automatic sizing of small runs; 0: phase kernels); no
+                                          reference counterpart */
 };
 
 /* ---- persistent state layout (export / import) ------------------------
@@ -230,6 +234,13 @@ typedef struct carl_env carl_env;
 /* Loads the arena mesh (env CARL_ARENA_OBJ, else carl_amd/assets/arena.obj next
  * to the library), allocates device state, resets every simulation to a
  * kickoff and packs the initial outputs.  frameskip >= 1.
+ * n_sim * (n_blue + n_orange) must be at most 6,628,032 cars: the state is
+ * addressed with 32-bit byte offsets.  A larger size fails with
+ * CARL_ERR_VALUE before any allocation.
+ * The arena is built once per process for each mesh (and metadata) file, and
+ * the environments on one device share one device copy of it, freed with the
+ * last of them (the reference builds its host mesh once per process,
+ * src/ArenaMesh.cu:17-28).
  * When the environment variable CARL_ARENA_METADATA is set, its file holds
  * RocketSim's native mesh metadata for every triangle (the text that
  * tools/arena_metadata.py writes: the triangle count, then per triangle

@@ -7,6 +7,10 @@ from pathlib import Path
 HEADER = Path(__file__).resolve().parents[1] / "include" / "carl_amd.h"
 
 
+def abi_header_text() -> str:
+    return HEADER.read_text()
+
+
 def enum_values(prefix: str) -> dict[str, int]:
     text = HEADER.read_text()
     return {m.group(1): int(m.group(2))

@@ -5,7 +5,7 @@ import ctypes as C
 
 import pytest
 
-from abi import CAR_NAMES, SIM_NAMES, declared_functions, enum_values
+from abi import CAR_NAMES, SIM_NAMES, abi_header_text, declared_functions, enum_values
 from carl_amd import build
 
 
@@ -53,6 +53,39 @@ def test_create_rejects_invalid_arguments_before_touching_the_device(lib, args, 
     assert rc == enum_values("CARL_")["CARL_ERR_VALUE"]
     assert handle.value is None
     assert message in lib.carl_last_error().decode()
+
+
+def _max_cars() -> int:
+    """The largest car count whose state the 32-bit buffer offsets reach: the
+    car block, 4 * CARL_CAR_FIELDS bytes per car in whole tiles of 64 cars,
+    stays below 2^31 bytes."""
+    return ((2 ** 31 - 1) // (4 * enum_values("CARL_")["CARL_CAR_FIELDS"])) & ~63
+
+
+def test_documented_size_limit_is_the_offset_limit():
+    import re
+
+    text = abi_header_text()
+    m = re.search(r"must be at most ([\d,]+) cars", text)
+    assert m and int(m.group(1).replace(",", "")) == _max_cars()
+
+
+@pytest.mark.parametrize("n_sim,blue,orange", [
+    (_max_cars() // 2 + 1, 1, 1),      # one 1v1 simulation past the limit
+    (_max_cars() // 8 + 1, 4, 4),      # 4v4
+    (_max_cars() + 1, 1, 0),           # one car per simulation
+    (2 ** 31 - 1, 4, 4),               # the car count itself overflows 32 bits
+])
+def test_create_rejects_sizes_past_the_32bit_offsets_before_any_allocation(lib, n_sim, blue, orange):
+    """Sizes whose state the engine's 32-bit buffer offsets cannot address fail
+    with CARL_ERR_VALUE and a message naming the limit; the check comes before
+    the arena build and any device call (none exists in this container)."""
+    handle = C.c_void_p()
+    rc = lib.carl_env_create(n_sim, blue, orange, 0, 1, 0, C.byref(handle))
+    assert rc == enum_values("CARL_")["CARL_ERR_VALUE"]
+    assert handle.value is None
+    err = lib.carl_last_error().decode()
+    assert f"at most {_max_cars()}" in err and str(n_sim * (blue + orange)) in err
 
 
 def test_null_handles_are_value_errors(lib):
