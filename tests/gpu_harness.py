@@ -115,6 +115,21 @@ class Pair:
                               f"(engine {a.reshape(-1)[i]!r}, oracle {b.reshape(-1)[i]!r})")
         return report
 
+    def fresh_output_mismatches(self) -> list[str]:
+        """output_mismatches after sync_oracle_from_engine: the transition
+        observation rows are written only for the simulations that finish in
+        a step (the others keep older rows, which the oracle never wrote), so
+        that buffer is compared on this step's finished rows."""
+        report = self.output_mismatches([n for n in OUTPUTS if n != "transition_obs"])
+        done = gpu_outputs(self.gpu)["dones"].reshape(-1).astype(bool)
+        a = torch.from_dlpack(self.gpu.get_transition_obs()).cpu().numpy().reshape(self.n_sim, -1)[done]
+        b = self.cpu.get("transition_obs").reshape(self.n_sim, -1)[done]
+        bad = np.nonzero((a.view(np.uint32) != b.view(np.uint32)).any(axis=1))[0]
+        if len(bad):
+            report.append(f"transition_obs: {len(bad)}/{int(done.sum())} finished rows differ, "
+                          f"first simulation {np.nonzero(done)[0][bad[0]]}")
+        return report
+
     def state_mismatches(self) -> list[str]:
         gc, gs, gt = gpu_state(self.gpu)
         oc, os_, ot = self.cpu.export_state()
@@ -124,6 +139,13 @@ class Pair:
         rep += describe_mismatch(CAR_NAMES, gc, oc)
         rep += describe_mismatch(SIM_NAMES, gs, os_)
         return rep
+
+    def import_state(self, car: np.ndarray, sim: np.ndarray, tick: int):
+        """Load one persistent state (include/carl_amd.h layout) into both sides."""
+        car = np.ascontiguousarray(car, dtype=np.uint32)
+        sim = np.ascontiguousarray(sim, dtype=np.uint32)
+        self.gpu.import_state(car.tobytes(), sim.tobytes(), int(tick))
+        self.cpu.import_state(car, sim, int(tick))
 
     def sync_oracle_from_engine(self):
         """Copy the engine's persistent state into the oracle."""
