@@ -268,6 +268,13 @@ def main() -> None:
                     help="print a markdown summary of rocprofv3 output directories of one bench run "
                          "(use - for an absent one; --steps/--warmup name its window, --copy-mib the copy size)")
     ap.add_argument("--copy-mib", type=int, default=512)
+    ap.add_argument("--clustered", action="store_true",
+                    help="start every simulation from a clustered scene (every car within 500 uu of the ball, "
+                         "at the floor, a wall or the ceiling) instead of half kickoffs, half random states")
+    ap.add_argument("--reset-fraction", type=float, default=0.0,
+                    help="after every step, reset this fraction of the simulations (a seeded Bernoulli mask) "
+                         "from random states through apply_reset_state(reset_mask=...); the masks and states "
+                         "come from pools made before timing")
     ap.add_argument("--stage-profile", action="store_true",
                     help="after the timed region, run further steps with the stage profile, print its table "
                          "on stderr and add it to the JSON line")
@@ -310,11 +317,21 @@ def main() -> None:
     if args.tick_window >= 0:
         env.tick_window = args.tick_window
 
-    odd = np.arange(1, n_sim, 2)
-    reset = workloads.random_reset_state(rng, len(odd), n_cars)
-    env.apply_reset_state(**{k: torch.from_numpy(v).to(dev) for k, v in reset.items()},
-                          simulation_indices=torch.from_numpy(odd.astype(np.int64)).to(dev))
+    if args.clustered:
+        reset = workloads.clustered_reset_state(rng, n_sim, n_cars)
+        env.apply_reset_state(**{k: torch.from_numpy(v).to(dev) for k, v in reset.items()})
+    else:
+        odd = np.arange(1, n_sim, 2)
+        reset = workloads.random_reset_state(rng, len(odd), n_cars)
+        env.apply_reset_state(**{k: torch.from_numpy(v).to(dev) for k, v in reset.items()},
+                              simulation_indices=torch.from_numpy(odd.astype(np.int64)).to(dev))
     pool = [torch.from_numpy(workloads.random_continuous_actions(rng, n_sim, n_cars)).to(dev) for _ in range(64)]
+    resets, masks = [], []
+    if args.reset_fraction > 0.0:
+        for _ in range(4):
+            resets.append({k: torch.from_numpy(v).to(dev)
+                           for k, v in workloads.random_reset_state(rng, n_sim, n_cars).items()})
+        masks = [torch.from_numpy(rng.uniform(0, 1, n_sim) < args.reset_fraction).to(dev) for _ in range(64)]
     team_sign = torch.tensor([1.0] * args.blue + [-1.0] * args.orange, device=dev)
     torch.cuda.synchronize()
 
@@ -322,7 +339,10 @@ def main() -> None:
         env.step_continuous(pool[i % len(pool)])
         with torch.cuda.stream(stream):
             score = torch.from_dlpack(env.get_rewards())
-            return (score[:, None] * team_sign).reshape(-1)  # default score reward
+            reward = (score[:, None] * team_sign).reshape(-1)  # default score reward
+        if resets:
+            env.apply_reset_state(**resets[i % len(resets)], reset_mask=masks[i % len(masks)])
+        return reward
 
     for i in range(args.warmup):
         env_step(i)
@@ -385,9 +405,12 @@ def main() -> None:
         "data": "synthetic",
         "env_steps_per_s": n_sim * args.steps / seconds,
         "config": {
-            "workload": (f"{args.blue}v{args.orange} n_sim={n_sim} tick_skip={args.tick_skip}: kickoff + seeded "
-                         "random states, seeded random continuous actions, obs/state packing, done resets, "
-                         "default score reward"),
+            "workload": (f"{args.blue}v{args.orange} n_sim={n_sim} tick_skip={args.tick_skip}: "
+                         + ("clustered scenes at the floor, walls and ceiling" if args.clustered
+                            else "kickoff + seeded random states")
+                         + ", seeded random continuous actions, obs/state packing, done resets, default score reward"
+                         + (f", {args.reset_fraction:.0%} of the simulations reset from random states after "
+                            "every step (masked apply_reset_state)" if args.reset_fraction > 0.0 else "")),
             "n_sim": n_sim,
             "n_cars": n_cars,
             "tick_skip": args.tick_skip,

@@ -643,9 +643,14 @@ __global__ void rewardsDonesKernel(Dev d, int tickCount, DoneRule rule, float* r
     tOvertime[s] = d.si(CARL_SIM_OVERTIME, s) != 0;
 }
 
-__global__ void matchKernel(Dev d, int* score, int* ticks, bool* overtime, const bool* mask)
+__global__ void matchKernel(Dev d, int* score, int* ticks, bool* overtime, const bool* mask, const int* list,
+                            const int* count)
 {
-    const int s = blockIdx.x * blockDim.x + threadIdx.x;
+    int s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (list) {
+        if (s >= *count) return;
+        s = list[s];
+    }
     if (s >= d.nSim || (mask && !mask[s])) return;
     score[s] = d.si(CARL_SIM_BLUE_SCORE, s) - d.si(CARL_SIM_ORANGE_SCORE, s);
     ticks[s] = d.si(CARL_SIM_EPISODE_TICKS, s);
@@ -770,6 +775,62 @@ __global__ __launch_bounds__(kPackBlock) void obsKernel(Dev d, float* out, int o
     packRowsParts(
         out, obsDimV, r0, min(r0 + packChunkRows(obsDimV), d.nTotal),
         [&](int a) { return !mask || mask[a / d.nCars]; },
+        [&](int a, int q, float* o) {
+            packObservationPart(d, a / d.nCars, a % d.nCars, invert != 0, normalizeObs != 0, prev != 0, q, o);
+        });
+}
+
+// Rows rowOf(i), i in [i0, i1), of out (rowLen floats each), built by
+// part(row, q, dst) for q = 0..kRowParts-1 as packRowsParts builds them, and
+// each stored as its own contiguous run (the rows of a compacted selection
+// are scattered through out).  Every thread of the workgroup calls this.
+template <typename RowOf, typename Part>
+DI void packRowsGathered(float* out, int rowLen, int i0, int i1, RowOf&& rowOf, Part&& part)
+{
+    extern __shared__ float packLds[];
+    __shared__ int rowAt[64];
+    const int t = threadIdx.x, lane = t & 63, q = t >> 6;
+    const int stride = packStride(rowLen), chunk = packChunkRows(rowLen);
+    const int rowStep = kPackBlock / rowLen, colStep = kPackBlock % rowLen;
+    for (int c0 = i0; c0 < i1; c0 += chunk) {
+        const int rows = min(chunk, i1 - c0);
+        const int row = lane < rows ? rowOf(c0 + lane) : 0;
+        if (q == 0) rowAt[lane] = row;
+        if (lane < rows) part(row, q, packLds + lane * stride);
+        __syncthreads();
+        const int total = rows * rowLen;
+        int rr = t / rowLen, c = t % rowLen;
+        for (int e = t; e < total; e += kPackBlock) {
+            __builtin_nontemporal_store(packLds[rr * stride + c], out + (size_t)rowAt[rr] * rowLen + c);
+            rr += rowStep;
+            c += colStep;
+            if (c >= rowLen) { c -= rowLen; rr++; }
+        }
+        __syncthreads();
+    }
+}
+
+// The state rows of the simulations list[0..*count).
+__global__ __launch_bounds__(kPackBlock) void stateListKernel(Dev d, float* out, int stateDimV, int touchWindow,
+                                                             int tickCount, const int* list, const int* count)
+{
+    const int i0 = blockIdx.x * packChunkRows(stateDimV), n = *count;
+    if (i0 >= n) return;
+    packRowsGathered(
+        out, stateDimV, i0, min(i0 + packChunkRows(stateDimV), n), [&](int i) { return list[i]; },
+        [&](int s, int q, float* o) { packStatePart(d, s, touchWindow, tickCount, q, o); });
+}
+
+// The observation rows of the cars of the simulations list[0..*count).
+__global__ __launch_bounds__(kPackBlock) void obsListKernel(Dev d, float* out, int obsDimV, int invert,
+                                                           int normalizeObs, int prev, const int* list,
+                                                           const int* count)
+{
+    const int i0 = blockIdx.x * packChunkRows(obsDimV), n = *count * d.nCars;
+    if (i0 >= n) return;
+    packRowsGathered(
+        out, obsDimV, i0, min(i0 + packChunkRows(obsDimV), n),
+        [&](int i) { return list[i / d.nCars] * d.nCars + i % d.nCars; },
         [&](int a, int q, float* o) {
             packObservationPart(d, a / d.nCars, a % d.nCars, invert != 0, normalizeObs != 0, prev != 0, q, o);
         });
@@ -911,10 +972,50 @@ __global__ __launch_bounds__(kPackBlock) void stepEnvKernel(Dev d, StepIO io)
     for (int w = t + kCopyRegs * kPackBlock; w < copyWords; w += kPackBlock) io.actionCopy[w0 + w] = io.actions[w0 + w];
 }
 
+// The rows a mask sets, compacted into list[0..*count): each thread scans
+// kCompactRows consecutive rows, a workgroup scan places the threads' rows,
+// and each workgroup takes its place in the list with one atomic add on the
+// count (which clearCountKernel zeroes first).  The workgroups' order in the
+// list varies from run to run; nothing depends on it, as every row's reset
+// and repacking touch that row's simulation only.
+__global__ void clearCountKernel(int* count) { *count = 0; }
+
+constexpr int kCompactBlock = 256;
+constexpr int kCompactRows = 16;
+__global__ __launch_bounds__(kCompactBlock) void compactMaskKernel(const uint8_t* __restrict__ mask, int n,
+                                                                   int* __restrict__ list, int* __restrict__ count)
+{
+    __shared__ int waveBase[kCompactBlock / 64 + 1];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int r0 = (blockIdx.x * kCompactBlock + t) * kCompactRows;
+    unsigned bits = 0;
+#pragma unroll
+    for (int k = 0; k < kCompactRows; k++)
+        if (r0 + k < n && mask[r0 + k] != 0) bits |= 1u << k;
+    const int c = __popc(bits);
+    const int incl = waveInclusiveScan(c);
+    if (lane == 63) waveBase[wave] = incl;
+    __syncthreads();
+    if (t == 0) {
+        int total = 0;
+        for (int w = 0; w < kCompactBlock / 64; w++) {
+            const int v = waveBase[w];
+            waveBase[w] = total;
+            total += v;
+        }
+        waveBase[kCompactBlock / 64] = total ? atomicAdd(count, total) : 0;
+    }
+    __syncthreads();
+    int at = waveBase[kCompactBlock / 64] + waveBase[wave] + incl - c;
+#pragma unroll
+    for (int k = 0; k < kCompactRows; k++)
+        if (bits & (1u << k)) list[at++] = r0 + k;
+}
+
 __global__ void setBallKernel(Dev d, const float* pos, const float* vel, const float* ang, Selection sel)
 {
-    const int r = blockIdx.x * blockDim.x + threadIdx.x;
-    if (r >= sel.n) return;
+    const int r = selectedInput(sel, blockIdx.x * blockDim.x + threadIdx.x);
+    if (r < 0) return;
     const int t = selectRow(sel, r, d.nSim);
     if (t < 0) return;
     d.ssetv(CARL_SIM_BALL_POS, t, V3{ pos[3 * r], pos[3 * r + 1], pos[3 * r + 2] });
@@ -927,11 +1028,13 @@ __global__ void setCarKernel(Dev d, const float* pos, const float* rot, const fl
                              const void* demoed, int byteDemoed, const float* boost, const float* internal,
                              Selection sel)
 {
-    const int src = blockIdx.x * blockDim.x + threadIdx.x;
-    if (src >= sel.n * d.nCars) return;
-    const int t = selectRow(sel, src / d.nCars, d.nSim);
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    const int r = selectedInput(sel, i / d.nCars);
+    if (r < 0) return;
+    const int t = selectRow(sel, r, d.nSim);
     if (t < 0) return;
-    setCarRow(d, src, t, src % d.nCars, pos, rot, vel, ang, demoed, byteDemoed != 0, boost, internal);
+    const int local = i % d.nCars;
+    setCarRow(d, r * d.nCars + local, t, local, pos, rot, vel, ang, demoed, byteDemoed != 0, boost, internal);
 }
 
 // Wheel contacts of the selected cars against the restored scene (rays only,
@@ -940,11 +1043,14 @@ __global__ __launch_bounds__(kContactBlock) void refreshKernel(Dev d, Selection 
 {
     __shared__ ContactLds L;
     const int lane = threadIdx.x;
-    const int src = blockIdx.x * kContactOwners + lane;
+    // a compacted selection's blocks past its cars have nothing to do
+    if (sel.list && blockIdx.x * kContactOwners >= *sel.count * d.nCars) return;
+    const int i = blockIdx.x * kContactOwners + lane;
     int car = -1;
-    if (lane < kContactOwners && src < sel.n * d.nCars) {
-        const int t = selectRow(sel, src / d.nCars, d.nSim);
-        if (t >= 0) car = t * d.nCars + src % d.nCars;
+    if (lane < kContactOwners) {
+        const int r = selectedInput(sel, i / d.nCars);
+        const int t = r < 0 ? -1 : selectRow(sel, r, d.nSim);
+        if (t >= 0) car = t * d.nCars + i % d.nCars;
     }
     const bool active = car >= 0 && !d.ci(CARL_CAR_DEMOED, car);
     V3 cen = kZero;
@@ -974,8 +1080,8 @@ __global__ __launch_bounds__(kContactBlock) void refreshKernel(Dev d, Selection 
 
 __global__ void setMatchKernel(Dev d, const int32_t* blue, const int32_t* orange, const int32_t* ticks, Selection sel)
 {
-    const int r = blockIdx.x * blockDim.x + threadIdx.x;
-    if (r >= sel.n) return;
+    const int r = selectedInput(sel, blockIdx.x * blockDim.x + threadIdx.x);
+    if (r < 0) return;
     const int t = selectRow(sel, r, d.nSim);
     if (t < 0) return;
     d.sseti(CARL_SIM_BLUE_SCORE, t, blue[r]);
@@ -987,8 +1093,8 @@ __global__ void setMatchKernel(Dev d, const int32_t* blue, const int32_t* orange
 
 __global__ void resetPadsKernel(Dev d, Selection sel)
 {
-    const int r = blockIdx.x * blockDim.x + threadIdx.x;
-    if (r >= sel.n) return;
+    const int r = selectedInput(sel, blockIdx.x * blockDim.x + threadIdx.x);
+    if (r < 0) return;
     const int t = selectRow(sel, r, d.nSim);
     if (t < 0) return;
     for (int p = 0; p < kPads; p++) d.ssetf(CARL_SIM_PAD_COOLDOWN + p, t, 0.f);
@@ -1292,6 +1398,7 @@ struct carl_env {
     int32_t* actions = nullptr;
     float* cactions = nullptr;
     uint32_t* ws = nullptr;  // per-tick car workspace (kWsPlanes planes)
+    int* rowList = nullptr;  // a masked reset's selected rows (n_sim), then their count
     float* ballScratch = nullptr;    // with it: kNativeMaxContacts slots of kNativeSlotWords per simulation
     int tickStreams = 1;                 // partitions of the tick, one stream each
     int contactScreen = 1;               // screen (car, triangle) pairs in the contact search
@@ -1353,7 +1460,7 @@ void freeAll(carl_env* e)
 {
     void* ptrs[] = { e->car, e->sim, e->obs, e->tobs, e->state, e->tstate, e->rewards, e->dones,
                      e->overtime, e->tovertime, e->score, e->ticks, e->tscore, e->tticks, e->actions, e->cactions,
-                     e->ws, e->prof, e->ballScratch };
+                     e->ws, e->prof, e->ballScratch, e->rowList };
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
     releaseArena(e->arena);
@@ -1559,7 +1666,24 @@ int packState(carl_env* e, float* out, int touchWindow, const bool* mask)
 
 int packMatch(carl_env* e, const bool* mask)
 {
-    matchKernel<<<e->grid(e->nSim, 64), 64, 0, e->stream>>>(e->dev(), e->score, e->ticks, e->overtime, mask);
+    matchKernel<<<e->grid(e->nSim, 64), 64, 0, e->stream>>>(e->dev(), e->score, e->ticks, e->overtime, mask,
+                                                             nullptr, nullptr);
+    HIP_TRY(hipGetLastError());
+    return CARL_OK;
+}
+
+// The outputs a reset changes (observations, state, match state) for the
+// simulations of a compacted selection.
+int packSelected(carl_env* e, const Selection& sel)
+{
+    obsListKernel<<<e->grid(e->nTotal, packChunkRows(e->obsDim)), kPackBlock, packLdsBytes(e->obsDim), e->stream>>>(
+        e->dev(), e->obs, e->obsDim, e->invert, e->normalize, e->prevControls, sel.list, sel.count);
+    HIP_TRY(hipGetLastError());
+    stateListKernel<<<e->grid(e->nSim, packChunkRows(e->stateDim)), kPackBlock, packLdsBytes(e->stateDim),
+                      e->stream>>>(e->dev(), e->state, e->stateDim, 1, e->tickCount, sel.list, sel.count);
+    HIP_TRY(hipGetLastError());
+    matchKernel<<<e->grid(e->nSim, 64), 64, 0, e->stream>>>(e->dev(), e->score, e->ticks, e->overtime, nullptr,
+                                                             sel.list, sel.count);
     HIP_TRY(hipGetLastError());
     return CARL_OK;
 }
@@ -1590,7 +1714,7 @@ int fullReset(carl_env* e)
     return initialPacks(e);
 }
 
-Selection makeSel(const int64_t* idx, const uint8_t* mask, int n) { return Selection{ idx, mask, n }; }
+Selection makeSel(const int64_t* idx, const uint8_t* mask, int n) { return Selection{ idx, mask, n, nullptr, nullptr }; }
 
 int setBallRows(carl_env* e, const float* pos, const float* vel, const float* ang, Selection sel)
 {
@@ -1718,6 +1842,7 @@ int carl_env_create(int nSim, int nBlue, int nOrange, int seed, int frameskip, i
     rc = rc ? rc : devAlloc(&e->actions, nT * 7);
     rc = rc ? rc : devAlloc(&e->cactions, nT * 7);
     rc = rc ? rc : devAlloc(&e->ws, (size_t)kWsPlanes * tiledItems(e->nTotal));
+    rc = rc ? rc : devAlloc(&e->rowList, nS + 1);
     if (e->native()) rc = rc ? rc : devAlloc(&e->ballScratch, (size_t)kNativeMaxContacts * kNativeSlotWords * nS);
     if (rc) return bail(rc);
 
@@ -1836,15 +1961,25 @@ int carl_env_apply_reset(carl_env* e, const float* bpos, const float* bvel, cons
     if (n == 0) return CARL_OK;
     if (!bpos || !bvel || !bang || !cpos || !crot || !cvel || !cang || !demoed)
         return fail(CARL_ERR_VALUE, "null reset input");
-    const Selection sel = makeSel(idx, mask, n);
+    Selection sel = makeSel(idx, mask, n);
+    if (mask) {
+        // the selected rows, compacted on the device: every kernel below
+        // runs over them only
+        sel.list = e->rowList;
+        sel.count = e->rowList + e->nSim;
+        clearCountKernel<<<1, 1, 0, e->stream>>>(e->rowList + e->nSim);
+        compactMaskKernel<<<e->grid(n, kCompactBlock * kCompactRows), kCompactBlock, 0, e->stream>>>(
+            mask, n, e->rowList, e->rowList + e->nSim);
+        HIP_TRY(hipGetLastError());
+    }
     CARL_TRY(resetPadRows(e, sel));
     CARL_TRY(setBallRows(e, bpos, bvel, bang, sel));
     CARL_TRY(setCarRows(e, cpos, crot, cvel, cang, demoed, byteDemoed, boost, internal, sel));
     if (hasMatch) CARL_TRY(setMatchRows(e, blue, orange, ticks, sel));
-    const bool* m = (const bool*)mask;
-    CARL_TRY(packObs(e, e->obs, m));
-    CARL_TRY(packState(e, e->state, 1, m));
-    CARL_TRY(packMatch(e, m));
+    if (mask) return packSelected(e, sel);
+    CARL_TRY(packObs(e, e->obs, nullptr));
+    CARL_TRY(packState(e, e->state, 1, nullptr));
+    CARL_TRY(packMatch(e, nullptr));
     return CARL_OK;
 }
 

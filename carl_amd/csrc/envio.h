@@ -433,11 +433,25 @@ DI void resetAfterDone(const Dev& d, int s, int tickCount, DoneRule rule, int nO
 
 // ----------------------------------------------------------------- setters
 
+// Input rows r < n, each targeting simulation indices[r] (r without
+// indices); with a mask only the rows it sets.  A masked selection may also
+// name its rows in a compacted list (ascending rows, list[0..*count) on the
+// device), so that the setters and the repacking run over the selected rows
+// only.
 struct Selection {
     const int64_t* indices;
     const uint8_t* mask;
     int n;
+    const int* list;
+    const int* count;
 };
+
+// the input row handled by work item i, or -1 past the selection
+DI int selectedInput(const Selection& sel, int i)
+{
+    if (sel.list) return i < *sel.count ? sel.list[i] : -1;
+    return i < sel.n ? i : -1;
+}
 
 // target simulation of input row r, or -1 when the row is skipped
 DI int selectRow(const Selection& sel, int r, int nSim)
