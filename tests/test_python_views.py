@@ -28,16 +28,43 @@ def _check_frames(q, forward, up, tol):
     np.testing.assert_allclose(_rotate(q, np.array([0, 0, 1.0])), up, atol=tol)
 
 
+# The conversion takes each component's magnitude from the square root of a
+# float32 diagonal combination of the rotation matrix (the reference's copysign
+# form): a component whose exact value is 0 comes out as the square root of
+# that sum's rounding residue, a few float32 ulps of 1, so components (and
+# the axes they rebuild) are exact to about sqrt(8 * 2^-24) / 2 = 3.5e-4.
+RESIDUE = 3.6e-4
+
+
 def test_quaternion_of_random_frames_reproduces_the_axes():
     rng = np.random.default_rng(0)
     q = rng.normal(size=(4096, 4))
     q /= np.linalg.norm(q, axis=-1, keepdims=True)
     forward, up = _rotate(q, np.array([1.0, 0, 0])), _rotate(q, np.array([0, 0, 1.0]))
     out = _forward_up_to_quat(torch.tensor(forward, dtype=torch.float32), torch.tensor(up, dtype=torch.float32))
-    _check_frames(out, forward, up, 2e-6)
+    _check_frames(out, forward, up, 4 * RESIDUE)
     # the same rotation as the generating quaternion, up to the sign of q
     canon = q * np.where(q[:, 3:] < 0, -1.0, 1.0)
-    np.testing.assert_allclose(out.double().numpy(), canon, atol=2e-6)
+    err = np.abs(out.double().numpy() - canon)
+    assert err.max() < RESIDUE, err.max()
+    # components well away from 0 carry no residue: float32 rounding only
+    far = np.abs(canon) > 0.05
+    assert err[far].max() < 2e-6, err[far].max()
+
+
+@pytest.mark.parametrize("yaw", [0.0, 0.3, 1.0, math.pi / 2, 2.5, -0.7, -math.pi / 2, -3.0])
+def test_quaternion_of_yaw_only_frames(yaw):
+    """A car on its wheels (up = +z) turned by `yaw`: z and w are the half
+    angle's sine and cosine; x and y, exactly 0, come out as the residue of
+    1 + R00 - R11 - R22 and 1 - R00 + R11 - R22, at most RESIDUE (the reference
+    conversion's behaviour)."""
+    forward = torch.tensor([[math.cos(yaw), math.sin(yaw), 0.0]], dtype=torch.float32)
+    up = torch.tensor([[0.0, 0.0, 1.0]], dtype=torch.float32)
+    out = _forward_up_to_quat(forward, up).double().numpy()[0]
+    exact = np.array([0.0, 0.0, math.sin(yaw / 2), math.cos(yaw / 2)])
+    exact *= 1.0 if exact[3] >= 0 else -1.0
+    assert np.abs(out[:2]).max() <= RESIDUE, out
+    assert np.abs(out[2:] - exact[2:]).max() < 1e-6, (out, exact)
 
 
 @pytest.mark.parametrize("axis,angle", [((1, 0, 0), math.pi), ((0, 1, 0), math.pi), ((0, 0, 1), math.pi),
@@ -45,12 +72,12 @@ def test_quaternion_of_random_frames_reproduces_the_axes():
                                         ((1, 0, 0), 3.0), ((1, 0, 0), -3.0)])
 def test_quaternion_of_half_turns_and_axis_rotations(axis, angle):
     """Rotations with w = 0 (half turns) and near it, where a conversion that
-    divides by w fails: the largest component must carry the division."""
+    divides by w fails."""
     a = np.array(axis, dtype=np.float64) / np.linalg.norm(axis)
     q = np.concatenate([a * math.sin(angle / 2), [math.cos(angle / 2)]])[None]
     forward, up = _rotate(q, np.array([1.0, 0, 0])), _rotate(q, np.array([0, 0, 1.0]))
     out = _forward_up_to_quat(torch.tensor(forward, dtype=torch.float32), torch.tensor(up, dtype=torch.float32))
-    _check_frames(out, forward, up, 1e-6)
+    _check_frames(out, forward, up, 4 * RESIDUE)
 
 
 def test_quaternion_renormalises_and_orthogonalises_the_basis():
@@ -58,7 +85,7 @@ def test_quaternion_renormalises_and_orthogonalises_the_basis():
     up = torch.tensor([[0.2, 0.0, 5.0], [0.0, 0.3, 1.0]])   # not orthogonal to forward
     out = _forward_up_to_quat(forward, up)
     f = forward.double().numpy() / np.linalg.norm(forward.numpy(), axis=-1, keepdims=True)
-    _check_frames(out, f, np.array([[0.0, 0, 1], [0.0, 0, 1]]), 1e-6)
+    _check_frames(out, f, np.array([[0.0, 0, 1], [0.0, 0, 1]]), 4 * RESIDUE)
 
 
 @pytest.mark.parametrize("forward,up,message", [
