@@ -297,7 +297,6 @@ std::string buildArena(const std::string& objPath, HostArena& out)
         const size_t nFine = (size_t)out.fineStart[kFineCells];
         out.fineRecords.assign(16 * nFine, 0.f);
         out.fineAux.assign(4 * nFine, 0.f);
-        out.fineTris.assign(nFine, 0);
         out.triAux.assign(4 * (size_t)nTris, 0.f);
         std::fill(fcount.begin(), fcount.end(), 0);
         for (int t = 0; t < nTris; t++) {
@@ -315,7 +314,42 @@ std::string buildArena(const std::string& objPath, HostArena& out)
                         const size_t f = (size_t)out.fineStart[c] + fcount[c]++;
                         std::memcpy(&out.fineRecords[16 * f], &out.triRecords[16 * (size_t)t], 16 * sizeof(float));
                         std::memcpy(&out.fineAux[4 * f], &out.triAux[4 * (size_t)t], 4 * sizeof(float));
-                        out.fineTris[f] = t;
+                    }
+        }
+    }
+    // car candidate grid: the same rule with the car's reach, triangle
+    // indices only, ascending within a cell
+    {
+        const double reach = (double)kCarGridReach;
+        auto carRange = [&](int t, int (&a)[3], int (&b)[3]) {
+            const double l[3] = { lo[t].x, lo[t].y, lo[t].z }, h[3] = { hi[t].x, hi[t].y, hi[t].z };
+            const double o[3] = { kArenaMin.x, kArenaMin.y, kArenaMin.z };
+            const int n[3] = { kCarX, kCarY, kCarZ };
+            for (int k = 0; k < 3; k++) {
+                a[k] = std::max(0, (int)std::floor((l[k] - reach - o[k]) / kCarCell));
+                b[k] = std::min(n[k] - 1, (int)std::floor((h[k] + reach - o[k]) / kCarCell));
+            }
+        };
+        std::vector<int> ccount(kCarCells + 1, 0);
+        for (int t = 0; t < nTris; t++) {
+            int a[3], b[3];
+            carRange(t, a, b);
+            for (int z = a[2]; z <= b[2]; z++)
+                for (int y = a[1]; y <= b[1]; y++)
+                    for (int x = a[0]; x <= b[0]; x++) ccount[x + kCarX * (y + kCarY * z)]++;
+        }
+        out.carStart.assign(kCarCells + 1, 0);
+        for (int c = 0; c < kCarCells; c++) out.carStart[c + 1] = out.carStart[c] + ccount[c];
+        out.carTris.assign((size_t)out.carStart[kCarCells], 0);
+        std::fill(ccount.begin(), ccount.end(), 0);
+        for (int t = 0; t < nTris; t++) {
+            int a[3], b[3];
+            carRange(t, a, b);
+            for (int z = a[2]; z <= b[2]; z++)
+                for (int y = a[1]; y <= b[1]; y++)
+                    for (int x = a[0]; x <= b[0]; x++) {
+                        const int c = x + kCarX * (y + kCarY * z);
+                        out.carTris[(size_t)out.carStart[c] + ccount[c]++] = t;
                     }
         }
     }

@@ -21,7 +21,8 @@ struct HostArena {
     std::vector<int> fineStart;     // kFineCells + 1 offsets into fineRecords (in references)
     std::vector<float> fineRecords; // 16 floats per ball-grid reference (record layout), ascending per cell
     std::vector<float> fineAux;     // 4 per ball-grid reference: edge angles xyz, registration range (bits)
-    std::vector<int> fineTris;      // triangle per ball-grid reference, ascending within a cell
+    std::vector<int> carStart;      // kCarCells + 1 offsets into carTris
+    std::vector<int> carTris;       // triangle per car-grid reference, ascending within a cell
     // native mesh metadata (only with CARL_ARENA_METADATA), 16 floats per
     // triangle: native vertex 0 xyz, order key (int bits, mesh * 10000 +
     // order); vertex 1 xyz, native mesh (int bits); vertex 2 xyz, edge flags

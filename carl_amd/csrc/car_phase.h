@@ -1041,13 +1041,13 @@ DI bool registeredIn(uint32_t reg, int bcell)
            y <= (int)((reg >> 18) & 63) && (int)((reg >> 24) & 15) <= z && z <= (int)(reg >> 28);
 }
 
-// The triangle of item q of owner o's run: an entry of a candidate-grid list
-// or of a broadphase cell's run (both in ascending triangle order).
+// The triangle of item q of owner o's run: an entry of a car-grid list or of
+// a broadphase cell's run (both in ascending triangle order).
 template <int Owners>
 DI int contactIndex(const Dev& d, const ContactLdsT<Owners>& L, int o, int q, bool valid)
 {
     const int ref = valid ? L.first[o] + q : 0;
-    return (L.fine[o] ? d.arena.fineTri : d.arena.cellTri)[ref];
+    return (L.fine[o] ? d.arena.carTri : d.arena.cellTri)[ref];
 }
 
 // The screening data of triangle `tri` for owner o, from the per-triangle

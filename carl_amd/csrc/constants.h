@@ -37,6 +37,18 @@ constexpr int kFineCells = kFineX * kFineY * kFineZ;
 static_assert(kFineX * kFineCell >= kArenaMax.x - kArenaMin.x && kFineY * kFineCell >= kArenaMax.y - kArenaMin.y &&
                   kFineZ * kFineCell >= kArenaMax.z - kArenaMin.z,
               "ball grid must cover the broadphase box");
+// car candidate grid: the same lists for the cars' contact search, in 32 uu
+// cells and with the car's own reach (every car test stays within 76.6 uu of
+// the car's centre, engine.hip), so a car near a curved wall walks about 30%
+// fewer candidates than in the ball's lists.  Each list is triangle indices
+// only (6.67 M references, 27 MB).
+constexpr float kCarCell = 32.f;
+constexpr float kCarGridReach = 78.f;
+constexpr int kCarX = 257, kCarY = 375, kCarZ = 66;   // ceil(extent / kCarCell)
+constexpr int kCarCells = kCarX * kCarY * kCarZ;
+static_assert(kCarX * kCarCell >= kArenaMax.x - kArenaMin.x && kCarY * kCarCell >= kArenaMax.y - kArenaMin.y &&
+                  kCarZ * kCarCell >= kArenaMax.z - kArenaMin.z,
+              "car grid must cover the broadphase box");
 
 // car
 constexpr V3 kHalf{ 60.186455f, 43.282655f, 19.262505f };

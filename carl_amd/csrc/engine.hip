@@ -122,15 +122,27 @@ struct SimRange {
 constexpr int kContactBlock = 64;
 static_assert(kContactOwners <= kContactBlock, "owners are lanes of the block");
 
-// The candidate-grid lists reach kBallRadius + kBallArenaBreak + 1 uu past
-// their cell; every car test stays closer to the car's centre: the box's
+// The car candidate grid's lists reach kCarGridReach uu past their cell;
+// every car test stays more than 1 uu closer to the car's centre: the box's
 // corners, and the wheel rays' ends (the rays start at the anchors, in the
-// centre's plane, and run along the car's down axis).
-constexpr float kGridReach = kBallRadius + kBallArenaBreak + 1.f;
+// centre's plane, and run along the car's down axis).  The 1 uu margin covers
+// the float rounding of the tests and of the centre's cell.
 constexpr float sq(float x) { return x * x; }
-static_assert(sq(kHalf.x) + sq(kHalf.y) + sq(kHalf.z) < sq(kGridReach), "car box beyond the candidate grid");
-static_assert(sq(kFrontX) + sq(kFrontY) + sq(kFrontRay + 1.f) < sq(kGridReach), "front rays beyond the grid");
-static_assert(sq(kBackX) + sq(kBackY) + sq(kBackRay + 1.f) < sq(kGridReach), "back rays beyond the grid");
+static_assert(sq(kHalf.x) + sq(kHalf.y) + sq(kHalf.z) < sq(kCarGridReach - 1.f), "car box beyond the car grid");
+static_assert(sq(kFrontX) + sq(kFrontY) + sq(kFrontRay + 1.f) < sq(kCarGridReach - 1.f), "front rays beyond the grid");
+static_assert(sq(kBackX) + sq(kBackY) + sq(kBackRay + 1.f) < sq(kCarGridReach - 1.f), "back rays beyond the grid");
+
+// the car-grid cell holding a car's centre (false outside the grid)
+DI bool carGridCell(V3 c, int& cell)
+{
+    const float x = (c.x - kArenaMin.x) / kCarCell;
+    const float y = (c.y - kArenaMin.y) / kCarCell;
+    const float z = (c.z - kArenaMin.z) / kCarCell;
+    if (!(x >= 0.f && x < (float)kCarX && y >= 0.f && y < (float)kCarY && z >= 0.f && z < (float)kCarZ))
+        return false;
+    cell = (int)x + kCarX * ((int)y + kCarY * (int)z);
+    return true;
+}
 
 // The contact search of cars [car0, car0 + Owners) (those below
 // carEnd) by one wave; L is that wave's own LDS.  Every lane of the wave calls
@@ -156,16 +168,16 @@ DI void contactGroup(const Dev& d, const Handoff& out, int screen, int car0, int
         demoed = d.ci(CARL_CAR_DEMOED, car) != 0;
         if (d.nCars == 2) ball = d.sv(CARL_SIM_BALL_POS, car >> 1);
         // the shorter of two lists that both hold every triangle the car can
-        // touch, in ascending triangle order: the candidate-grid list of the
-        // cell holding the car's centre (every triangle within ball reach +
-        // 1 uu of the cell; the car's tests reach less far; its items count
-        // when registered in the broadphase cell), and the broadphase cell's
-        // run itself.  Both orders agree on the triangles that count, so the
-        // tie-breaks by run position pick the same triangle.
+        // touch, in ascending triangle order: the car-grid list of the cell
+        // holding the car's centre (every triangle within kCarGridReach of
+        // the cell; its items count when registered in the broadphase cell),
+        // and the broadphase cell's run itself.  Both orders agree on the
+        // triangles that count, so the tie-breaks by triangle pick the same
+        // triangle.
         int fcell;
-        const bool inGrid = ballGridCell(cen, fcell);
-        const int fFirst = inGrid ? d.arena.fineStart[fcell] : 0;
-        const int fCount = inGrid ? d.arena.fineStart[fcell + 1] - fFirst : 0;
+        const bool inGrid = carGridCell(cen, fcell);
+        const int fFirst = inGrid ? d.arena.carStart[fcell] : 0;
+        const int fCount = inGrid ? d.arena.carStart[fcell + 1] - fFirst : 0;
         fine = inGrid && fCount < bp.count;
         first = fine ? fFirst : bp.start;
         count = fine ? fCount : bp.count;
@@ -1309,7 +1321,8 @@ int uploadArena(const HostArena& host, DeviceArena* a)
     CARL_TRY(uploadBlock(a, host.triAux.data(), bytes(host.triAux), &v.triAux));
     CARL_TRY(uploadBlock(a, host.fineRecords.data(), bytes(host.fineRecords), &v.fineRec));
     CARL_TRY(uploadBlock(a, host.fineAux.data(), bytes(host.fineAux), &v.fineAux));
-    CARL_TRY(uploadBlock(a, host.fineTris.data(), bytes(host.fineTris), &v.fineTri));
+    CARL_TRY(uploadBlock(a, host.carStart.data(), bytes(host.carStart), &v.carStart));
+    CARL_TRY(uploadBlock(a, host.carTris.data(), bytes(host.carTris), &v.carTri));
     CARL_TRY(uploadBlock(a, host.fineStart.data(), bytes(host.fineStart), &v.fineStart));
     v.native = nullptr;
     if (!host.nativeRecords.empty())

@@ -42,8 +42,9 @@ struct ArenaView {
     const float4* triAux;    // per triangle: edge angles xyz, packed broadphase registration range
     const float4* fineRec;   // 4 per ball-grid reference (record layout)
     const float4* fineAux;   // per ball-grid reference: edge angles xyz, packed broadphase registration range
-    const int* fineTri;      // triangle per ball-grid reference, ascending within a cell
     const int* fineStart;    // kFineCells + 1 offsets into fineRec (in references)
+    const int* carStart;     // kCarCells + 1 offsets into carTri
+    const int* carTri;       // triangle per car-grid reference, ascending within a cell
     const float4* native;    // 4 per triangle, native mesh metadata (arena.h); null without it
 };
 
