@@ -262,6 +262,9 @@ def main() -> None:
     ap.add_argument("--tick-window", type=int, default=-1,
                     help="simulations per workgroup of the tick-window kernel, 0 for phase kernels "
                          "(-1: engine default)")
+    ap.add_argument("--tick-balance", type=int, default=-1, choices=(-1, 0, 1),
+                    help="1v1 window launches dealt to the workgroups by the last launch's contact work "
+                         "(1), or workgroups of consecutive simulations (0); -1: engine default")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (HBM counter calibration) and exit")
     ap.add_argument("--summarize-rocprof", nargs=5, metavar=("TRACE", "FETCH", "WRITE", "COPY_FETCH", "COPY_WRITE"),
@@ -316,6 +319,8 @@ def main() -> None:
         env.tick_streams = args.tick_streams
     if args.tick_window >= 0:
         env.tick_window = args.tick_window
+    if args.tick_balance >= 0:
+        env.tick_balance = args.tick_balance
 
     if args.clustered:
         reset = workloads.clustered_reset_state(rng, n_sim, n_cars)
@@ -417,6 +422,7 @@ def main() -> None:
             "parallelism": "single GPU",
             "tick_streams": parts,
             "tick_window": env.tick_window_launch,
+            "balanced_deal": env.tick_balanced_launch,
             "timed_steps": f"env steps {args.warmup + 1}..{args.warmup + args.steps} after the initial reset",
         },
         "roofline": {

@@ -653,6 +653,10 @@ PYBIND11_MODULE(_carl, m)
         .def_property("tick_window", [](Env& e) { return e.param(CARL_PARAM_TICK_WINDOW); },
                       [](Env& e, int v) { e.setParam(CARL_PARAM_TICK_WINDOW, v); })
         .def_property_readonly("tick_window_launch", [](Env& e) { return e.param(CARL_PARAM_TICK_WINDOW_LAUNCH); })
+        .def_property("tick_balance", [](Env& e) { return e.param(CARL_PARAM_TICK_BALANCE); },
+                      [](Env& e, int v) { e.setParam(CARL_PARAM_TICK_BALANCE, v); })
+        .def_property_readonly("tick_balanced_launch",
+                               [](Env& e) { return e.param(CARL_PARAM_TICK_BALANCED_LAUNCH) != 0; })
         .def_property_readonly("obs_dim", [](Env& e) { return e.param(CARL_PARAM_OBS_DIM); })
         .def_property_readonly("act_dim", [](Env& e) { return e.param(CARL_PARAM_ACT_DIM); })
         .def_property_readonly("action_nvec", &Env::actionNvec)

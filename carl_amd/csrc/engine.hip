@@ -144,17 +144,27 @@ DI bool carGridCell(V3 c, int& cell)
     return true;
 }
 
-// The contact search of cars [car0, car0 + Owners) (those below
-// carEnd) by one wave; L is that wave's own LDS.  Every lane of the wave calls
-// it; it synchronises the wave only.  The candidates' triangle indices are
-// loaded Lead + 1 rounds of 64 items ahead of the screen, their screening
-// data one round ahead.
+// What a contact search cost its lane: the candidate items its car walked
+// (none for a demolished car), whether its box met the arena (a SAT hit,
+// whose contact generation is the search's costliest part) and, in 1v1,
+// whether the simulation's two cars were close enough for their pair test to
+// go past the distance check soon.
+struct WalkCost {
+    int items;
+    bool sat;
+    bool near;
+};
+
+// The contact search of one car per lane (car, where ok) by one wave; L is
+// that wave's own LDS.  Every lane of the wave calls it; it synchronises the
+// wave only.  The candidates' triangle indices are loaded Lead + 1 rounds of
+// 64 items ahead of the screen, their screening data one round ahead.  In
+// 1v1 the cars of a simulation must sit in lanes 2i and 2i + 1.
 template <int Lead, int Owners, class Handoff>
-DI void contactGroup(const Dev& d, const Handoff& out, int screen, int car0, int carEnd, ContactLdsT<Owners>& L,
-                     int lane)
+DI WalkCost contactGroup(const Dev& d, const Handoff& out, int screen, int car, bool ok, ContactLdsT<Owners>& L,
+                         int lane)
 {
-    const int car = car0 + lane;
-    const bool ok = lane < Owners && car < carEnd;
+    ok = ok && lane < Owners;
     V3 cen = kZero;
     Q4 rot{ 0.f, 0.f, 0.f, 1.f };
     Broad bp{ 0, 0, 0 };
@@ -190,6 +200,7 @@ DI void contactGroup(const Dev& d, const Handoff& out, int screen, int car0, int
         [&](const RefBox& b, int o, int) { contactScreen(L, b, o, lane); },
         [&](bool last) { contactDrain(d, L, lane, last); });
     waveSync();
+    const bool satHit = ok && lane < Owners && L.satHits[lane] > 0;
     // 1v1: the other car of an owner's simulation is the neighbouring lane's
     // owner (owner groups start at even cars and end at even ones), so its
     // pre-tick box and flag come from that lane's registers, and the ball's
@@ -222,7 +233,12 @@ DI void contactGroup(const Dev& d, const Handoff& out, int screen, int car0, int
     // every lane's reads of the search area come before any lane's handoff
     // writes (an LDS handoff may share that area)
     waveSync();
-    if (!ok) return;
+    if (!ok) return WalkCost{ 0, false, false };
+    // two car boxes within twice the box diagonal of each other (the pair
+    // test's distance bound), with the travel of a window on top
+    const float near = 4.f * len(kHalf);
+    const WalkCost cost{ demoed ? 0 : count, satHit,
+                         d.nCars == 2 && !demoed && !odemoed && lensq(ocen - cen) < near * near };
 #pragma unroll
     for (int k = 0; k < kWheels; k++) {
         out.put(kWsDist + k, car, lane, __float_as_uint(w.dist[k]));
@@ -236,13 +252,15 @@ DI void contactGroup(const Dev& d, const Handoff& out, int screen, int car0, int
 #pragma unroll
         for (int i = 0; i < 10; i++) out.put(kWsMan + i, car, lane, __float_as_uint(pt[i]));
     }
+    return cost;
 }
 
 __global__ __launch_bounds__(kContactBlock) void contactKernel(Dev d, uint32_t* __restrict__ ws, int screen, SimRange range)
 {
     __shared__ ContactLds L;
-    contactGroup<1, kContactOwners>(d, WsHandoff{ ws, d.nTotal }, screen, range.begin * d.nCars + blockIdx.x * kContactOwners, range.end * d.nCars, L,
-                    threadIdx.x);
+    const int car = range.begin * d.nCars + blockIdx.x * kContactOwners + (int)threadIdx.x;
+    contactGroup<1, kContactOwners>(d, WsHandoff{ ws, d.nTotal }, screen, car, car < range.end * d.nCars, L,
+                                    threadIdx.x);
 }
 
 // A2: controls, car-arena contacts, suspension and the contact solve.
@@ -315,15 +333,14 @@ DI void carCarSim(const Dev& d, int sim, int tick)
 constexpr int kBallBlock = 64;
 constexpr int kBallOwners = 32;
 
-// Simulations [sim0, sim0 + kBallOwners) (those below simEnd) by one wave; L
-// is that wave's own LDS.  Every lane of the wave calls it; it synchronises
-// the wave only.  With Native (arena metadata) each owner lane gathers and
-// solves its ball against the native meshes alone.
+// One simulation per lane of the first kBallOwners (sim, where ok) by one
+// wave; L is that wave's own LDS.  Every lane of the wave calls it; it
+// synchronises the wave only.  With Native (arena metadata) each owner lane
+// gathers and solves its ball against the native meshes alone.
 template <bool Native>
-DI void ballGroup(const Dev& d, int tick, int sim0, int simEnd, BallLds& L, int lane)
+DI void ballGroup(const Dev& d, int tick, int sim, bool ok, BallLds& L, int lane)
 {
-    const int sim = sim0 + lane;
-    const bool ok = lane < kBallOwners && sim < simEnd;
+    ok = ok && lane < kBallOwners;
     if constexpr (Native) {
         if (ok) {
             carCarSim(d, sim, tick);
@@ -378,14 +395,16 @@ DI void ballGroup(const Dev& d, int tick, int sim0, int simEnd, BallLds& L, int 
 __global__ __launch_bounds__(kBallBlock) void ballKernel(Dev d, int tick, SimRange range)
 {
     __shared__ BallLds L;
-    ballGroup<false>(d, tick, range.begin + blockIdx.x * kBallOwners, range.end, L, threadIdx.x);
+    const int sim = range.begin + blockIdx.x * kBallOwners + (int)threadIdx.x;
+    ballGroup<false>(d, tick, sim, sim < range.end, L, threadIdx.x);
 }
 
 // the same with the native arena meshes
 __global__ __launch_bounds__(kBallBlock) void ballNativeKernel(Dev d, int tick, SimRange range)
 {
     __shared__ BallLds L;
-    ballGroup<true>(d, tick, range.begin + blockIdx.x * kBallOwners, range.end, L, threadIdx.x);
+    const int sim = range.begin + blockIdx.x * kBallOwners + (int)threadIdx.x;
+    ballGroup<true>(d, tick, sim, sim < range.end, L, threadIdx.x);
 }
 
 // C + D: integration and impulse caches of every car and ball, then the
@@ -476,6 +495,65 @@ enum ProfWord {
     kProfWords
 };
 
+// Balanced 1v1 launches deal the simulations to the workgroups in units of
+// kUnitSims consecutive simulations: slot s of workgroup b (wave 2 b + s / 4,
+// lanes 16 (s % 4) .. + 15 for the cars, 8 (s % 4) .. + 7 for the balls)
+// holds one unit.  Simulations share nothing, so the deal changes no result;
+// it is made so that the workgroups finish together.
+//
+// The deal needs no pass of its own.  At its last tick every launch files
+// each unit under the class of its cost (dealClass) in an output list: one
+// atomic per unit on a count, then the unit at that position of the list.
+// Each class has kDealSubs lists, unit u going to list u % kDealSubs, so
+// that units of equal cost (the kickoffs, early on) do not all wait on one
+// count.  The next launch reads the lists back in rank order, costliest
+// class first (any order within a class), and deals them to the
+// waves in rounds: round 0 gives the costliest units, one to each wave in
+// order; every later round gives its units in reverse order, so that the
+// waves holding the costliest units get the cheapest of each round (the
+// costs have a long tail: a car whose box meets the arena every tick, a pair
+// that may collide).  Two units of pairs that may collide thus fall to the
+// two waves of one workgroup, whose pair solves run side by side.  Three
+// list sets rotate: launch L reads set L % 3, files into set (L + 1) % 3
+// (cleared by launch L - 1) and clears the counts of set (L + 2) % 3, which
+// no launch touches again before L + 1.
+constexpr int kUnitSims = 8;
+constexpr int kBalancedSims = 64;                        // simulations per balanced workgroup
+constexpr int kUnitSlots = kBalancedSims / kUnitSims;   // units per balanced workgroup
+constexpr int kWaveUnits = kUnitSlots / 2;              // units per wave
+constexpr int kDealClasses = 32;
+constexpr int kDealSubs = 8;
+constexpr int kDealLists = kDealClasses * kDealSubs;
+constexpr int kDealSets = 3;
+// A unit's cost is its contact work in the launch's last tick, in candidate
+// items (each about 0.04 us of its wave's time).  A car whose box met the
+// arena costs its wave about 6 us of contact generation (160 items),
+// counted at half, kSatCost, since it persists less from one launch to the
+// next than a candidate count does; a pair that may collide (cars within
+// twice their box diagonal) costs about 25 us per tick of its serial solve,
+// kPairCost items.  (The cost summed over the launch's ticks ranked the
+// units no better.)
+constexpr int kSatCost = 80;
+constexpr int kPairCost = 720;
+
+// cost class: four classes per doubling from 8 items up (class 0 below)
+DI int dealClass(int cost)
+{
+    if (cost < 8) return 0;
+    return min(kDealClasses - 1, 1 + (int)(4.f * __log2f((float)cost * (1.f / 8.f))));
+}
+
+// list k = kDealSubs c + j of a set holds up to nUnits / kDealSubs units
+// from outList + k nUnits / kDealSubs, its count at outCount[k]
+struct WindowMap {
+    const int* inCount;   // the deal's counts and lists (null: slot s of workgroup b holds unit 8 b + s)
+    const int* inList;
+    int* outCount;        // this launch's filing
+    int* outList;
+    int* clearCount;      // the counts the next launch files into
+    int nUnits;
+};
+
 // The window kernel's body.  With Profile, thread 0 of each workgroup reads
 // the wall clock (the constant-rate counter) at the start and after every
 // phase barrier; a phase's time runs from the barrier before it to its own,
@@ -483,15 +561,68 @@ enum ProfWord {
 // the kProfStages sums, and the launch's last workgroup to finish adds its
 // own phase times, its start delay and the launch's span.  Without Profile
 // the code is the plain kernel.
-template <bool Profile, bool Native, int Cars>
+template <bool Profile, bool Native, int Cars, bool Balanced>
 DI void tickWindowBody(Dev d0, uint32_t* __restrict__ ws, int screen, int kind, const void* __restrict__ actions,
-                       int tick0, int ticks, int simsPerBlock, SimRange range, unsigned long long* __restrict__ prof)
+                       int tick0, int ticks, int simsPerBlock, SimRange range, WindowMap map,
+                       unsigned long long* __restrict__ prof)
 {
+    static_assert(!Balanced || Cars == 2, "balanced launches are 1v1");
+    static_assert(kWindowBlock == 2 * 64 && kWaveUnits * 2 * kUnitSims == 64 && kWaveUnits * kUnitSims == kBallOwners,
+                  "a balanced wave holds kWaveUnits units: 64 cars, kBallOwners balls");
     // a fixed car count (Cars > 0) lets every per-simulation loop fold
     Dev d = d0;
     if constexpr (Cars > 0) d.nCars = Cars;
     __shared__ WindowLds L;
+    __shared__ int unit[Balanced ? kUnitSlots : 1];
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    // balanced: the car of thread (or contact owner) i, the simulation of
+    // workgroup position j (ball owners, finish and pads)
+    auto slotCar = [&](int i) { return unit[i >> 4] * (2 * kUnitSims) + (i & 15); };
+    auto slotSim = [&](int j) { return unit[j >> 3] * kUnitSims + (j & 7); };
+    if constexpr (Balanced) {
+        if (map.inCount) {
+            // the lists' first ranks, costliest class first, in the LDS the
+            // contact phase takes over afterwards; each thread scans two
+            static_assert(kDealLists == 2 * kWindowBlock && kDealLists * sizeof(int) <= sizeof(WaveLds),
+                          "the deal's scan: two lists per thread, in one wave's LDS");
+            int* first = reinterpret_cast<int*>(&L.wave[0]);
+            __shared__ int waveSum[kWindowWaves];
+            const int k0 = 2 * t;   // lists k0, k0 + 1 in rank order: class kDealClasses - 1 - k / kDealSubs
+            auto countOf = [&](int k) { return map.inCount[(kDealClasses - 1 - k / kDealSubs) * kDealSubs + k % kDealSubs]; };
+            const int n0 = countOf(k0), n1 = countOf(k0 + 1);
+            int incl = n0 + n1;
+            for (int o = 1; o < 64; o <<= 1) {
+                const int y = __shfl_up(incl, o);
+                if (lane >= o) incl += y;
+            }
+            if (lane == 63) waveSum[wave] = incl;
+            __syncthreads();
+            int before = 0;
+            for (int v = 0; v < wave; v++) before += waveSum[v];
+            first[k0] = before + incl - n0 - n1;
+            first[k0 + 1] = before + incl - n1;
+            __syncthreads();
+            if (t < kUnitSlots) {
+                const int waves = map.nUnits / kWaveUnits, wv = 2 * blockIdx.x + t / kWaveUnits, r = t % kWaveUnits;
+                const int rank = r == 0 ? wv : r * waves + (waves - 1 - wv);
+                // the last list whose first rank is at most rank
+                int lo = 0;
+                for (int step = kDealLists / 2; step > 0; step >>= 1)
+                    if (lo + step < kDealLists && first[lo + step] <= rank) lo += step;
+                const int per = map.nUnits / kDealSubs;
+                const int k = (kDealClasses - 1 - lo / kDealSubs) * kDealSubs + lo % kDealSubs;
+                unit[t] = map.inList[(size_t)k * per + min(rank - first[lo], per - 1)];
+            }
+            __syncthreads();   // the scan's LDS is the contact phase's
+        } else if (t < kUnitSlots) {
+            unit[t] = blockIdx.x * kUnitSlots + t;
+        }
+        if (blockIdx.x == 0) {
+            map.clearCount[2 * t] = 0;
+            map.clearCount[2 * t + 1] = 0;
+        }
+        __syncthreads();
+    }
     const int sim0 = range.begin + blockIdx.x * simsPerBlock;
     const int simEnd = min(sim0 + simsPerBlock, range.end);
     const int car0 = sim0 * d.nCars, carEnd = simEnd * d.nCars;
@@ -510,31 +641,66 @@ DI void tickWindowBody(Dev d0, uint32_t* __restrict__ ws, int screen, int kind, 
     }
     for (int k = 0; k < ticks; k++) {
         const int tick = tick0 + k;
-        for (int g = car0 + wave * kWindowContactOwners; g < carEnd; g += kWindowWaves * kWindowContactOwners)
-            contactGroup<kWindowContactLead, kWindowContactOwners>(d, LdsHandoff{ L.wave[wave].hand }, screen, g,
-                                                                     carEnd, L.wave[wave].contact, lane);
+        if constexpr (Balanced) {
+            const WalkCost c = contactGroup<kWindowContactLead, kWindowContactOwners>(
+                d, LdsHandoff{ L.wave[wave].hand }, screen, slotCar(t), true, L.wave[wave].contact, lane);
+            if (k == ticks - 1) {
+                // the unit's cost for the next deal (a pair counted at its first car)
+                int w = c.items + (c.sat ? kSatCost : 0) + (c.near && (lane & 1) == 0 ? kPairCost : 0);
+                w += __shfl_xor(w, 8);
+                w += __shfl_xor(w, 4);
+                w += __shfl_xor(w, 2);
+                w += __shfl_xor(w, 1);
+                if ((lane & 15) == 0) {
+                    const int u = unit[t >> 4], l = dealClass(w) * kDealSubs + u % kDealSubs;
+                    map.outList[(size_t)l * (map.nUnits / kDealSubs) + atomicAdd(&map.outCount[l], 1)] = u;
+                }
+            }
+        } else {
+            for (int g = car0 + wave * kWindowContactOwners; g < carEnd; g += kWindowWaves * kWindowContactOwners)
+                contactGroup<kWindowContactLead, kWindowContactOwners>(d, LdsHandoff{ L.wave[wave].hand }, screen,
+                                                                         g + lane, g + lane < carEnd,
+                                                                         L.wave[wave].contact, lane);
+        }
         __syncthreads();
         mark(kStageContact);
-        for (int c = car0 + t; c < carEnd; c += kWindowBlock)
-            carArenaCar(d, LdsHandoff{ L.wave[wave].hand }, kind, actions, tick, c, lane);
+        if constexpr (Balanced) {
+            carArenaCar(d, LdsHandoff{ L.wave[wave].hand }, kind, actions, tick, slotCar(t), lane);
+        } else {
+            for (int c = car0 + t; c < carEnd; c += kWindowBlock)
+                carArenaCar(d, LdsHandoff{ L.wave[wave].hand }, kind, actions, tick, c, lane);
+        }
         __syncthreads();
         mark(kStageCarArena);
-        {
+        if constexpr (Balanced) {
+            ballGroup<Native>(d, tick, slotSim(kBallOwners * wave + (lane & 31)), lane < kBallOwners,
+                              L.wave[wave].ball, lane);
+        } else {
             // the block's simulations split evenly between the waves (a
             // block of 21 3v3 or 32 2v2 simulations would otherwise leave
             // the second wave idle): at most kBallOwners per wave and group
             const int per = (simEnd - sim0 + kWindowWaves - 1) / kWindowWaves;
             const int wEnd = min(sim0 + (wave + 1) * per, simEnd);
             for (int g = sim0 + wave * per; g < wEnd; g += kBallOwners)
-                ballGroup<Native>(d, tick, g, min(g + kBallOwners, wEnd), L.wave[wave].ball, lane);
+                ballGroup<Native>(d, tick, g + lane, g + lane < wEnd, L.wave[wave].ball, lane);
         }
         __syncthreads();
         mark(kStageBall);
-        for (int c = car0 + t; c < carEnd; c += kWindowBlock) finishCar(d, c);
-        for (int s = sim0 + t; s < simEnd; s += kWindowBlock) finishBall(d, s);
+        if constexpr (Balanced) {
+            finishCar(d, slotCar(t));
+            if (t < kBalancedSims) finishBall(d, slotSim(t));
+        } else {
+            for (int c = car0 + t; c < carEnd; c += kWindowBlock) finishCar(d, c);
+            for (int s = sim0 + t; s < simEnd; s += kWindowBlock) finishBall(d, s);
+        }
         __syncthreads();
         mark(kStageFinish);
-        {
+        if constexpr (Balanced) {
+            int tp = t;
+            asm volatile("" : "+v"(tp));
+            const int q = tp / kBalancedSims, j = tp - q * kBalancedSims;
+            boostPadsRange(d, slotSim(j), kPads * q / 2, kPads * (q + 1) / 2);
+        } else {
             // boost pads: the workgroup's threads split into kWindowBlock /
             // simsPerBlock parts, each taking a contiguous range of every
             // simulation's pads (in 1v1 two parts, one wave each).  The
@@ -575,26 +741,28 @@ DI void tickWindowBody(Dev d0, uint32_t* __restrict__ ws, int screen, int kind, 
 // two waves per SIMD (the second bound is waves per execution unit): 256
 // VGPRs.  Cars > 0: instantiated for that many cars per simulation (1v1, the
 // common case, measured 6% faster than the same kernel with the count
-// read at run time; 2v2 and 3v3 5% and 3%); 0: any count.
-template <int Cars>
+// read at run time; 2v2 and 3v3 5% and 3%); 0: any count.  Balanced: the
+// 1v1 instance that takes its simulations from the deal (WindowMap).
+template <int Cars, bool Balanced>
 __global__ __launch_bounds__(kWindowBlock, 2) void tickWindowKernel(Dev d, uint32_t* __restrict__ ws, int screen,
                                                                  int kind, const void* __restrict__ actions,
                                                                  int tick0, int ticks, int simsPerBlock,
-                                                                 SimRange range)
+                                                                 SimRange range, WindowMap map)
 {
-    tickWindowBody<false, false, Cars>(d, ws, screen, kind, actions, tick0, ticks, simsPerBlock, range, nullptr);
+    tickWindowBody<false, false, Cars, Balanced>(d, ws, screen, kind, actions, tick0, ticks, simsPerBlock, range,
+                                                 map, nullptr);
 }
 
-using WindowKernel = void (*)(Dev, uint32_t*, int, int, const void*, int, int, int, SimRange);
+using WindowKernel = void (*)(Dev, uint32_t*, int, int, const void*, int, int, int, SimRange, WindowMap);
 
 // the instance for a car count: 1v1, 2v2 and 3v3 have their own
-WindowKernel windowKernelFor(int nCars)
+WindowKernel windowKernelFor(int nCars, bool balanced)
 {
     switch (nCars) {
-    case 2: return tickWindowKernel<2>;
-    case 4: return tickWindowKernel<4>;
-    case 6: return tickWindowKernel<6>;
-    default: return tickWindowKernel<0>;
+    case 2: return balanced ? tickWindowKernel<2, true> : tickWindowKernel<2, false>;
+    case 4: return tickWindowKernel<4, false>;
+    case 6: return tickWindowKernel<6, false>;
+    default: return tickWindowKernel<0, false>;
     }
 }
 
@@ -602,32 +770,37 @@ WindowKernel windowKernelFor(int nCars)
 __global__ __launch_bounds__(kWindowBlock, 2) void tickWindowNativeKernel(Dev d, uint32_t* __restrict__ ws,
                                                                        int screen, int kind,
                                                                        const void* __restrict__ actions, int tick0,
-                                                                       int ticks, int simsPerBlock, SimRange range)
+                                                                       int ticks, int simsPerBlock, SimRange range,
+                                                                       WindowMap map)
 {
-    tickWindowBody<false, true, 0>(d, ws, screen, kind, actions, tick0, ticks, simsPerBlock, range, nullptr);
+    tickWindowBody<false, true, 0, false>(d, ws, screen, kind, actions, tick0, ticks, simsPerBlock, range, map,
+                                          nullptr);
 }
 
 // the same kernel with the stage profile
-template <int Cars>
+template <int Cars, bool Balanced>
 __global__ __launch_bounds__(kWindowBlock, 2) void tickWindowProfileKernel(Dev d, uint32_t* __restrict__ ws,
                                                                         int screen, int kind,
                                                                         const void* __restrict__ actions, int tick0,
                                                                         int ticks, int simsPerBlock, SimRange range,
+                                                                        WindowMap map,
                                                                         unsigned long long* __restrict__ prof)
 {
-    tickWindowBody<true, false, Cars>(d, ws, screen, kind, actions, tick0, ticks, simsPerBlock, range, prof);
+    tickWindowBody<true, false, Cars, Balanced>(d, ws, screen, kind, actions, tick0, ticks, simsPerBlock, range,
+                                                map, prof);
 }
 
-using ProfileKernel = void (*)(Dev, uint32_t*, int, int, const void*, int, int, int, SimRange, unsigned long long*);
+using ProfileKernel = void (*)(Dev, uint32_t*, int, int, const void*, int, int, int, SimRange, WindowMap,
+                               unsigned long long*);
 
 // the profiled twin of windowKernelFor's instance for a car count
-ProfileKernel profileKernelFor(int nCars)
+ProfileKernel profileKernelFor(int nCars, bool balanced)
 {
     switch (nCars) {
-    case 2: return tickWindowProfileKernel<2>;
-    case 4: return tickWindowProfileKernel<4>;
-    case 6: return tickWindowProfileKernel<6>;
-    default: return tickWindowProfileKernel<0>;
+    case 2: return balanced ? tickWindowProfileKernel<2, true> : tickWindowProfileKernel<2, false>;
+    case 4: return tickWindowProfileKernel<4, false>;
+    case 6: return tickWindowProfileKernel<6, false>;
+    default: return tickWindowProfileKernel<0, false>;
     }
 }
 
@@ -1412,6 +1585,12 @@ struct carl_env {
     float* cactions = nullptr;
     uint32_t* ws = nullptr;  // per-tick car workspace (kWsPlanes planes)
     int* rowList = nullptr;  // a masked reset's selected rows (n_sim), then their count
+    // 1v1: the deal of balanced window launches, kDealSets sets of class
+    // counts and lists, and the balanced launches so far
+    int* dealCount = nullptr;
+    int* dealList = nullptr;
+    long long dealLaunches = 0;
+    int balance = 1;                     // deal 1v1 window launches by cost
     float* ballScratch = nullptr;    // with it: kNativeMaxContacts slots of kNativeSlotWords per simulation
     int tickStreams = 1;                 // partitions of the tick, one stream each
     int contactScreen = 1;               // screen (car, triangle) pairs in the contact search
@@ -1473,7 +1652,7 @@ void freeAll(carl_env* e)
 {
     void* ptrs[] = { e->car, e->sim, e->obs, e->tobs, e->state, e->tstate, e->rewards, e->dones,
                      e->overtime, e->tovertime, e->score, e->ticks, e->tscore, e->tticks, e->actions, e->cactions,
-                     e->ws, e->prof, e->ballScratch, e->rowList };
+                     e->ws, e->prof, e->ballScratch, e->rowList, e->dealCount, e->dealList };
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
     releaseArena(e->arena);
@@ -1588,6 +1767,15 @@ int effectiveWindowSims(const carl_env* e)
     return wsb;
 }
 
+// Whether the next window launch deals its simulations by cost: 1v1 on the
+// mesh arena, one partition, workgroups of kBalancedSims simulations, all
+// of them full.
+bool balancedLaunch(const carl_env* e)
+{
+    return e->balance && e->nCars == 2 && !e->native() && e->dealList && std::min(e->tickStreams, e->nSim) == 1
+           && effectiveWindowSims(e) == kBalancedSims && e->nSim % kBalancedSims == 0;
+}
+
 int launchTicks(carl_env* e, int kind, const void* actions, int n)
 {
     if (n <= 0) return CARL_OK;
@@ -1606,6 +1794,20 @@ int launchTicks(carl_env* e, int kind, const void* actions, int n)
     }
     if (e->windowSims > 0) {
         const int wsb = effectiveWindowSims(e);
+        const bool balanced = balancedLaunch(e);
+        WindowMap map{};
+        if (balanced) {
+            // the first balanced launch deals the identity
+            const int nU = e->nSim / kUnitSims;
+            const long long l = e->dealLaunches++;
+            auto set = [&](long long k, int* base, size_t per) { return base + (size_t)(k % kDealSets) * per; };
+            map.inCount = l > 0 ? set(l, e->dealCount, kDealLists) : nullptr;
+            map.inList = l > 0 ? set(l, e->dealList, (size_t)kDealClasses * nU) : nullptr;
+            map.outCount = set(l + 1, e->dealCount, kDealLists);
+            map.outList = set(l + 1, e->dealList, (size_t)kDealClasses * nU);
+            map.clearCount = set(l + 2, e->dealCount, kDealLists);
+            map.nUnits = nU;
+        }
         for (int p = 0; p < parts; p++) {
             const SimRange r = range[p];
             const bool timed = p == 0;
@@ -1615,16 +1817,16 @@ int launchTicks(carl_env* e, int kind, const void* actions, int n)
                 const int slots = std::min(blocks, e->profResident);
                 if (e->profSlots != 0 && e->profSlots != slots) e->profMixed = true;
                 e->profSlots = slots;
-                CARL_MARK(launchTick(e, timed, CARL_KERNEL_WINDOW, profileKernelFor(e->nCars),
+                CARL_MARK(launchTick(e, timed, CARL_KERNEL_WINDOW, profileKernelFor(e->nCars, balanced),
                                      dim3(blocks),
                                      dim3(kWindowBlock), 0, stream[p], d, e->ws, e->contactScreen, kind, actions,
-                                     e->tickCount + 1, n, wsb, r, e->prof));
+                                     e->tickCount + 1, n, wsb, r, map, e->prof));
             } else {
                 CARL_MARK(launchTick(e, timed, CARL_KERNEL_WINDOW,
-                                     e->native() ? tickWindowNativeKernel : windowKernelFor(e->nCars),
+                                     e->native() ? tickWindowNativeKernel : windowKernelFor(e->nCars, balanced),
                                      dim3(blocks),
                                      dim3(kWindowBlock), 0, stream[p], d, e->ws, e->contactScreen, kind, actions,
-                                     e->tickCount + 1, n, wsb, r));
+                                     e->tickCount + 1, n, wsb, r, map));
             }
         }
     }
@@ -1832,7 +2034,7 @@ int carl_env_create(int nSim, int nBlue, int nOrange, int seed, int frameskip, i
         if (hipGetDevice(&device) != hipSuccess
             || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess
             || hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                   &perCu, windowKernelFor(e->nCars), kWindowBlock, 0) != hipSuccess)
+                   &perCu, windowKernelFor(e->nCars, false), kWindowBlock, 0) != hipSuccess)
             return bail(fail(CARL_ERR_RUNTIME, "window kernel occupancy query failed"));
         e->windowResident = perCu * cus;
     }
@@ -1856,6 +2058,10 @@ int carl_env_create(int nSim, int nBlue, int nOrange, int seed, int frameskip, i
     rc = rc ? rc : devAlloc(&e->cactions, nT * 7);
     rc = rc ? rc : devAlloc(&e->ws, (size_t)kWsPlanes * tiledItems(e->nTotal));
     rc = rc ? rc : devAlloc(&e->rowList, nS + 1);
+    if (e->nCars == 2 && nS % kBalancedSims == 0) {
+        rc = rc ? rc : devAlloc(&e->dealCount, (size_t)kDealSets * kDealLists);
+        rc = rc ? rc : devAlloc(&e->dealList, (size_t)kDealSets * kDealClasses * (nS / kUnitSims));
+    }
     if (e->native()) rc = rc ? rc : devAlloc(&e->ballScratch, (size_t)kNativeMaxContacts * kNativeSlotWords * nS);
     if (rc) return bail(rc);
 
@@ -2075,6 +2281,10 @@ int carl_env_set_param(carl_env* e, int p, int v)
         e->windowSims = v;
         e->windowAuto = false;
         return CARL_OK;
+    case CARL_PARAM_TICK_BALANCE:
+        if (v != 0 && v != 1) return fail(CARL_ERR_VALUE, "tick_balance must be 0 or 1");
+        e->balance = v;
+        return CARL_OK;
     default: return fail(CARL_ERR_VALUE, "parameter is read-only or unknown");
     }
 }
@@ -2100,6 +2310,8 @@ int carl_env_get_param(carl_env* e, int p, int* v)
     case CARL_PARAM_TICK_WINDOW: *v = e->windowSims; break;
     case CARL_PARAM_TICK_WINDOW_LAUNCH: *v = effectiveWindowSims(e); break;
     case CARL_PARAM_NATIVE_ARENA: *v = e->native(); break;
+    case CARL_PARAM_TICK_BALANCE: *v = e->balance; break;
+    case CARL_PARAM_TICK_BALANCED_LAUNCH: *v = balancedLaunch(e); break;
     default: return fail(CARL_ERR_VALUE, "unknown parameter");
     }
     return CARL_OK;
@@ -2126,7 +2338,8 @@ int carl_env_enable_timing(carl_env* e, int enable)
         HIP_TRY(hipGetDevice(&device));
         HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
         HIP_TRY(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, device));
-        HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(&perCu, profileKernelFor(e->nCars), kWindowBlock, 0));
+        HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(&perCu, profileKernelFor(e->nCars, false), kWindowBlock,
+                                                             0));
         if (khz <= 0 || perCu <= 0) return fail(CARL_ERR_RUNTIME, "no wall-clock rate or window occupancy");
         e->profResident = perCu * cus;
         e->clockMHz = khz / 1000.0;

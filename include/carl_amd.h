@@ -129,10 +129,20 @@ enum {
                                       counterpart */
     CARL_PARAM_NATIVE_ARENA = 14,  /* read-only: 1 when the environment was created with native mesh
                                       metadata (the reference's ArenaMesh::hasNativeMetadata) */
-    CARL_PARAM_TICK_WINDOW_LAUNCH = 15 /* read-only: simulations per workgroup the next window launch
+    CARL_PARAM_TICK_WINDOW_LAUNCH = 15, /* read-only: simulations per workgroup the next window launch
                                           uses (CARL_PARAM_TICK_WINDOW capped at 128 cars, after the
                                           automatic sizing of small runs; 0: phase kernels); no
                                           reference counterpart */
+    CARL_PARAM_TICK_BALANCE = 16,  /* 1: 1v1 window launches of 64-simulation workgroups deal the
+                                      simulations to the workgroups in units of 8, ordered by the
+                                      contact work each unit did in the balanced launch before, so
+                                      that the workgroups finish together; 0: workgroup b takes
+                                      simulations [64 b, 64 b + 64).  Results are identical; no
+                                      reference counterpart (default 1) */
+    CARL_PARAM_TICK_BALANCED_LAUNCH = 17 /* read-only: 1 when the next window launch is dealt (1v1,
+                                            one partition, 64-simulation workgroups, n_sim a
+                                            multiple of 64, mesh arena, CARL_PARAM_TICK_BALANCE
+                                            on); no reference counterpart */
 };
 
 /* ---- persistent state layout (export / import) ------------------------

@@ -12,7 +12,8 @@ rows of the simulations that finish in the step: the others keep rows from
 steps the oracle did not run):
   * the headline workload, 1v1 at 65,536 simulations with frameskip 8, after
     300 steps, in the production launch shape (64 simulations per window
-    workgroup);
+    workgroup, dealt to the workgroups by the contact work of the step
+    before);
   * the clustered 3v3 workload at 16,384 simulations (every car within
     500 uu of the ball, at the floor, the walls or the ceiling), compared for
     its first three steps and again after 100 steps.
@@ -50,7 +51,8 @@ def test_headline_workload_after_300_steps(gpu):
     rng = np.random.default_rng(300)
     n = 65536
     p = Pair(n, 1, 1, seed=1, frameskip=8)
-    assert p.gpu.tick_window_launch == 64      # the production launch shape
+    assert p.gpu.tick_window_launch == 64      # the production launch shape,
+    assert p.gpu.tick_balanced_launch          # its simulations dealt to the workgroups by cost
     odd = np.arange(1, n, 2)
     p.apply_reset_state(workloads.random_reset_state(rng, len(odd), 2), simulation_indices=odd.astype(np.int64))
     _engine_steps(p, rng, 300)

@@ -19,16 +19,19 @@ from abi import CAR_NAMES, SIM_NAMES
 pytestmark = pytest.mark.gpu
 
 
-def _run_both(n, n_blue, n_orange, frameskip, steps, make_state, seed, window=64, streams=4, reset_every=0):
+def _run_both(n, n_blue, n_orange, frameskip, steps, make_state, seed, window=64, streams=4, reset_every=0,
+              balanced=False):
     rng = np.random.default_rng(seed)
     nc = n_blue + n_orange
     fused = carl_amd.Env(n, n_blue, n_orange, 5, frameskip, True, False, True)
     phased = carl_amd.Env(n, n_blue, n_orange, 5, frameskip, True, False, True)
     fused.tick_window = window
     fused.tick_streams = streams
+    fused.tick_balance = int(balanced)
     phased.tick_window = 0
     phased.tick_streams = streams
     assert (fused.tick_window, phased.tick_window) == (window, 0)
+    assert fused.tick_balanced_launch == balanced
     state = {k: dev(v) for k, v in make_state(rng, n, nc).items()}
     for env in (fused, phased):
         env.apply_reset_state(**state)
@@ -68,6 +71,34 @@ def test_window_dense_geometry_3v3_and_2v2(gpu):
 
 def test_window_per_tick_steps_with_masked_resets(gpu):
     _run_both(4096, 2, 2, 1, 40, workloads.random_reset_state, seed=45, reset_every=1)
+
+
+@pytest.mark.parametrize("make_state,reset_every", [(workloads.random_reset_state, 0),
+                                                     (workloads.clustered_reset_state, 3)])
+def test_balanced_deal_1v1(gpu, make_state, reset_every):
+    """Balanced 1v1 launches take their simulations in units of eight, dealt
+    by the contact work of the launch before: the deal moves simulations
+    between workgroups from step to step, never a result.  Clustered states
+    put most cars against the walls, so the deal reorders heavily."""
+    _run_both(8192, 1, 1, 8, 30, make_state, seed=48, streams=1, reset_every=reset_every, balanced=True)
+
+
+def test_balanced_launch_conditions(gpu):
+    """The deal runs only for 1v1 in one partition with full workgroups of 64."""
+    env = carl_amd.Env(4096, 1, 1, 1, 8, True, False, False)
+    env.tick_window, env.tick_streams = 64, 1
+    assert env.tick_balance == 1 and env.tick_balanced_launch
+    for attr, value in (("tick_streams", 2), ("tick_window", 32), ("tick_balance", 0)):
+        setattr(env, attr, value)
+        assert not env.tick_balanced_launch, attr
+        env.tick_window, env.tick_streams, env.tick_balance = 64, 1, 1
+        assert env.tick_balanced_launch
+    for n, blue, orange in ((4032 + 8, 1, 1), (2048, 2, 2), (2048, 1, 0)):  # a partial workgroup, 2v2, one car
+        other = carl_amd.Env(n, blue, orange, 1, 8, True, False, False)
+        other.tick_window, other.tick_streams = 64, 1
+        assert not other.tick_balanced_launch, (n, blue, orange)
+    with pytest.raises(ValueError):
+        env.tick_balance = 2
 
 
 def test_window_single_car(gpu):
