@@ -496,10 +496,13 @@ enum ProfWord {
 };
 
 // Balanced 1v1 launches deal the simulations to the workgroups in units of
-// kUnitSims consecutive simulations: slot s of workgroup b (wave 2 b + s / 4,
-// lanes 16 (s % 4) .. + 15 for the cars, 8 (s % 4) .. + 7 for the balls)
-// holds one unit.  Simulations share nothing, so the deal changes no result;
-// it is made so that the workgroups finish together.
+// kUnitSims consecutive simulations: slot s of workgroup b (wave
+// 2 b + s / kWaveUnits) holds one unit, its cars in kUnitCars consecutive
+// lanes and its balls in kUnitSims.  Simulations share nothing, so the deal
+// changes no result; it is made so that the workgroups finish together.  A
+// unit's cars fill whole 128-byte lines of every car field (units of 8
+// simulations left half lines to workgroups on other XCDs, whose L2s then
+// fetched the same lines: the launch read 2.5 times the bytes).
 //
 // The deal needs no pass of its own.  At its last tick every launch files
 // each unit under the class of its cost (dealClass) in an output list: one
@@ -517,13 +520,15 @@ enum ProfWord {
 // list sets rotate: launch L reads set L % 3, files into set (L + 1) % 3
 // (cleared by launch L - 1) and clears the counts of set (L + 2) % 3, which
 // no launch touches again before L + 1.
-constexpr int kUnitSims = 8;
+constexpr int kUnitSims = 16;   // 32 cars: one 128-byte line of each car field
 constexpr int kBalancedSims = 64;                        // simulations per balanced workgroup
+constexpr int kUnitCars = 2 * kUnitSims;
 constexpr int kUnitSlots = kBalancedSims / kUnitSims;   // units per balanced workgroup
 constexpr int kWaveUnits = kUnitSlots / 2;              // units per wave
 constexpr int kDealClasses = 32;
-constexpr int kDealSubs = 8;
+constexpr int kDealSubs = 4;
 constexpr int kDealLists = kDealClasses * kDealSubs;
+constexpr int kListsPerThread = kDealLists / 128;   // of a balanced workgroup's threads, in the deal's scan
 constexpr int kDealSets = 3;
 // A unit's cost is its contact work in the launch's last tick, in candidate
 // items (each about 0.04 us of its wave's time).  A car whose box met the
@@ -567,7 +572,7 @@ DI void tickWindowBody(Dev d0, uint32_t* __restrict__ ws, int screen, int kind, 
                        unsigned long long* __restrict__ prof)
 {
     static_assert(!Balanced || Cars == 2, "balanced launches are 1v1");
-    static_assert(kWindowBlock == 2 * 64 && kWaveUnits * 2 * kUnitSims == 64 && kWaveUnits * kUnitSims == kBallOwners,
+    static_assert(kWindowBlock == 2 * 64 && kWaveUnits * kUnitCars == 64 && kWaveUnits * kUnitSims == kBallOwners,
                   "a balanced wave holds kWaveUnits units: 64 cars, kBallOwners balls");
     // a fixed car count (Cars > 0) lets every per-simulation loop fold
     Dev d = d0;
@@ -577,30 +582,39 @@ DI void tickWindowBody(Dev d0, uint32_t* __restrict__ ws, int screen, int kind, 
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
     // balanced: the car of thread (or contact owner) i, the simulation of
     // workgroup position j (ball owners, finish and pads)
-    auto slotCar = [&](int i) { return unit[i >> 4] * (2 * kUnitSims) + (i & 15); };
-    auto slotSim = [&](int j) { return unit[j >> 3] * kUnitSims + (j & 7); };
+    auto slotCar = [&](int i) { return unit[i / kUnitCars] * kUnitCars + i % kUnitCars; };
+    auto slotSim = [&](int j) { return unit[j / kUnitSims] * kUnitSims + j % kUnitSims; };
     if constexpr (Balanced) {
         if (map.inCount) {
             // the lists' first ranks, costliest class first, in the LDS the
-            // contact phase takes over afterwards; each thread scans two
-            static_assert(kDealLists == 2 * kWindowBlock && kDealLists * sizeof(int) <= sizeof(WaveLds),
-                          "the deal's scan: two lists per thread, in one wave's LDS");
+            // contact phase takes over afterwards; each thread scans
+            // kListsPerThread of them: lists k in rank order hold class
+            // kDealClasses - 1 - k / kDealSubs
+            static_assert(kListsPerThread * kWindowBlock == kDealLists && kDealLists * sizeof(int) <= sizeof(WaveLds),
+                          "the deal's scan: whole lists per thread, in one wave's LDS");
             int* first = reinterpret_cast<int*>(&L.wave[0]);
             __shared__ int waveSum[kWindowWaves];
-            const int k0 = 2 * t;   // lists k0, k0 + 1 in rank order: class kDealClasses - 1 - k / kDealSubs
-            auto countOf = [&](int k) { return map.inCount[(kDealClasses - 1 - k / kDealSubs) * kDealSubs + k % kDealSubs]; };
-            const int n0 = countOf(k0), n1 = countOf(k0 + 1);
-            int incl = n0 + n1;
+            int n[kListsPerThread], sum = 0;
+#pragma unroll
+            for (int i = 0; i < kListsPerThread; i++) {
+                const int k = kListsPerThread * t + i;
+                n[i] = map.inCount[(kDealClasses - 1 - k / kDealSubs) * kDealSubs + k % kDealSubs];
+                sum += n[i];
+            }
+            int incl = sum;
             for (int o = 1; o < 64; o <<= 1) {
                 const int y = __shfl_up(incl, o);
                 if (lane >= o) incl += y;
             }
             if (lane == 63) waveSum[wave] = incl;
             __syncthreads();
-            int before = 0;
-            for (int v = 0; v < wave; v++) before += waveSum[v];
-            first[k0] = before + incl - n0 - n1;
-            first[k0 + 1] = before + incl - n1;
+            int r = incl - sum;
+            for (int v = 0; v < wave; v++) r += waveSum[v];
+#pragma unroll
+            for (int i = 0; i < kListsPerThread; i++) {
+                first[kListsPerThread * t + i] = r;
+                r += n[i];
+            }
             __syncthreads();
             if (t < kUnitSlots) {
                 const int waves = map.nUnits / kWaveUnits, wv = 2 * blockIdx.x + t / kWaveUnits, r = t % kWaveUnits;
@@ -618,8 +632,8 @@ DI void tickWindowBody(Dev d0, uint32_t* __restrict__ ws, int screen, int kind, 
             unit[t] = blockIdx.x * kUnitSlots + t;
         }
         if (blockIdx.x == 0) {
-            map.clearCount[2 * t] = 0;
-            map.clearCount[2 * t + 1] = 0;
+#pragma unroll
+            for (int i = 0; i < kListsPerThread; i++) map.clearCount[kListsPerThread * t + i] = 0;
         }
         __syncthreads();
     }
@@ -647,12 +661,9 @@ DI void tickWindowBody(Dev d0, uint32_t* __restrict__ ws, int screen, int kind, 
             if (k == ticks - 1) {
                 // the unit's cost for the next deal (a pair counted at its first car)
                 int w = c.items + (c.sat ? kSatCost : 0) + (c.near && (lane & 1) == 0 ? kPairCost : 0);
-                w += __shfl_xor(w, 8);
-                w += __shfl_xor(w, 4);
-                w += __shfl_xor(w, 2);
-                w += __shfl_xor(w, 1);
-                if ((lane & 15) == 0) {
-                    const int u = unit[t >> 4], l = dealClass(w) * kDealSubs + u % kDealSubs;
+                for (int o = kUnitCars / 2; o > 0; o >>= 1) w += __shfl_xor(w, o);
+                if (lane % kUnitCars == 0) {
+                    const int u = unit[t / kUnitCars], l = dealClass(w) * kDealSubs + u % kDealSubs;
                     map.outList[(size_t)l * (map.nUnits / kDealSubs) + atomicAdd(&map.outCount[l], 1)] = u;
                 }
             }

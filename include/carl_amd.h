@@ -134,7 +134,7 @@ enum {
                                           automatic sizing of small runs; 0: phase kernels); no
                                           reference counterpart */
     CARL_PARAM_TICK_BALANCE = 16,  /* 1: 1v1 window launches of 64-simulation workgroups deal the
-                                      simulations to the workgroups in units of 8, ordered by the
+                                      simulations to the workgroups in units of 16, ordered by the
                                       contact work each unit did in the balanced launch before, so
                                       that the workgroups finish together; 0: workgroup b takes
                                       simulations [64 b, 64 b + 64).  Results are identical; no

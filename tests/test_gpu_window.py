@@ -76,7 +76,7 @@ def test_window_per_tick_steps_with_masked_resets(gpu):
 @pytest.mark.parametrize("make_state,reset_every", [(workloads.random_reset_state, 0),
                                                      (workloads.clustered_reset_state, 3)])
 def test_balanced_deal_1v1(gpu, make_state, reset_every):
-    """Balanced 1v1 launches take their simulations in units of eight, dealt
+    """Balanced 1v1 launches take their simulations in units of sixteen, dealt
     by the contact work of the launch before: the deal moves simulations
     between workgroups from step to step, never a result.  Clustered states
     put most cars against the walls, so the deal reorders heavily."""
