@@ -60,10 +60,14 @@ def describe_mismatch(names, a, b, limit=8) -> list[str]:
 
 class Pair:
     def __init__(self, n_sim, n_blue, n_orange, seed=7, frameskip=1, invert_orange=True, normalize=False,
-                 previous_controls=False):
+                 previous_controls=False, obj_path=None):
+        """obj_path: the oracle's arena mesh (the engine reads CARL_ARENA_OBJ,
+        which the caller sets to the same file)."""
         self.gpu = carl_amd.Env(n_sim, n_blue, n_orange, seed, frameskip, invert_orange, normalize,
                                 previous_controls)
-        self.cpu = OracleEnv(n_sim, n_blue, n_orange, seed, frameskip, invert_orange, normalize, previous_controls)
+        kw = {} if obj_path is None else {"obj_path": obj_path}
+        self.cpu = OracleEnv(n_sim, n_blue, n_orange, seed, frameskip, invert_orange, normalize, previous_controls,
+                             **kw)
         self.n_sim, self.n_cars = n_sim, n_blue + n_orange
 
     def close(self):

@@ -518,10 +518,10 @@ def _seam_expected(n, N, Nb, E):
       concave seam (the neighbour turns toward the contact side, its angle
         below 0): a normal pointing out of both faces becomes N; any other
         normal stays
-      convex seam (angle above 0): a normal beyond the neighbour's normal
-        is turned about E onto the neighbour's angle (its E component kept),
-        if it then still points out of the contact triangle; any other
-        normal stays
+      convex seam (angle above 0): a normal pointing behind both faces
+        stays; a normal beyond the neighbour's normal is turned about E onto
+        the neighbour's angle (its E component kept), if it then still
+        points out of the contact triangle; any other normal stays
     Returns (expected normal, branch name, distance of the inputs from a
     decision boundary)."""
     u = np.cross(E, N)
@@ -531,6 +531,8 @@ def _seam_expected(n, N, Nb, E):
         if n @ N > 0.0 and n @ Nb > 0.0:
             return N, "concave: onto the face", margin
         return n, "concave: kept", margin
+    if n @ N < 0.0 and n @ Nb < 0.0:
+        return n, "convex: kept (behind both faces)", min(abs(n @ N), abs(n @ Nb))
     theta = np.arctan2(n @ u, n @ N)
     if theta > beta:
         turned = _rotate_about(n, E, beta - theta)
@@ -678,3 +680,114 @@ def test_manifold_normals_at_seams_between_non_coplanar_triangles():
     for branch in ("concave: onto the face", "convex: turned onto the neighbour", "convex: kept (inside the cone)",
                    "normal changed"):
         assert branches.get(branch, 0) >= 5, branches
+
+
+def _wedge_obj(path, phi, theta, z=300.0, size=300.0):
+    """A two-triangle mesh away from every analytic plane: T1 = (A, B, C)
+    level at height z, its edges AB (along +x) and BC open (no neighbour),
+    the angle at A between AB and AC phi; T2 shares CA and folds down across
+    it by theta (a convex seam).  A point of AB at x = A.x + s lies
+    s sin(phi) from the seam's line.  OBJ vertex lines list (y, x, z), as
+    the arena file does."""
+    a = np.array([0.0, 0.0, z])
+    u = np.array([np.cos(phi), np.sin(phi), 0.0])      # along AC
+    w = np.array([-np.sin(phi), np.cos(phi), 0.0])     # level, away from T1 across AC
+    pts = [a, a + [size, 0.0, 0.0], a + size * u,
+           a + 0.5 * size * u + 0.7 * size * (w * np.cos(theta) - np.array([0.0, 0.0, 1.0]) * np.sin(theta))]
+    path.write_text("\n".join(f"v {p[1]:.6f} {p[0]:.6f} {p[2]:.6f}" for p in pts) + "\nf 1 2 3\nf 1 3 4\n")
+    return a
+
+
+def wedge_trials(obj, apex, theta_deg, trials, seed):
+    """Random car poses pressed into the open edge AB of a wedge mesh
+    (`_wedge_obj`) near its apex, from above or from below, run through the
+    oracle.  Yields, for each pose whose deepest clip contact lies on T1 (and
+    is deep enough and far enough from a tie with T2 to hold in float32):
+    the car's position and rotation, the contact's distance from the seam,
+    the normal the manifold should keep there (`_seam_expected` within 5 uu,
+    the clip normal beyond), the manifold's normal, and a category."""
+    from oracle_py import OracleEnv
+
+    env = OracleEnv(1, 1, 0, 3, obj_path=obj)
+    verts, tris, angles, _, _ = env.arena()
+    assert len(tris) == 2
+    seam = [e for e in range(3) if abs(angles[0][e]) < 2 * np.pi]
+    assert len(seam) == 1 and 0.0 < angles[0][seam[0]] < np.pi
+    a, b = verts[tris[0][seam[0]]].astype(np.float64), verts[tris[0][(seam[0] + 1) % 3]].astype(np.float64)
+    E, N, Nb = (b - a) / np.linalg.norm(b - a), _tri_normal(verts, tris, 0), _tri_normal(verts, tris, 1)
+    rng = np.random.default_rng(seed)
+    for trial in range(trials):
+        # the apex angle is 150 degrees: a point of AB at s lies s / 2 from the seam
+        p = apex + [rng.uniform(6.0, 14.0) if theta_deg < 90 else rng.uniform(2.0, 25.0), 0.0, 0.0]
+        q = rng.normal(size=4)
+        q = np.float32(q / np.linalg.norm(q)).astype(np.float64)
+        pos = p + [0.0, 0.0, 100.0]
+        env.set_car(pos[None, None], q[None, None], np.zeros((1, 1, 3)), np.zeros((1, 1, 3)), np.zeros((1, 1), bool))
+        car, _, _ = env.export_state()
+        cen, r = f32c(car, "CEN"), _rot(f32c(car, "ROT", 4))
+        heights = (CORNERS @ r.T)[:, 2]
+        if trial % 2:      # from below: the highest corner just above the edge, the box under the open side
+            corner, target = CORNERS[int(np.argmax(heights))], p + [0.0, rng.uniform(-5.0, 1.0), rng.uniform(0.2, 2.0)]
+        else:              # from above: the lowest corner just below
+            corner, target = CORNERS[int(np.argmin(heights))], p + [0.0, rng.uniform(-30.0, 5.0), -rng.uniform(0.2, 2.0)]
+        pos = np.float32(pos + target - (cen + r @ corner)).astype(np.float64)
+        env.set_car(pos[None, None], q[None, None], np.zeros((1, 1, 3)), np.zeros((1, 1, 3)), np.zeros((1, 1), bool))
+        car, _, _ = env.export_state()
+        cen, r = f32c(car, "CEN"), _rot(f32c(car, "ROT", 4))
+        best, deepest = None, [-np.inf, -np.inf]
+        for t in range(2):
+            local = ((verts[tris[t]].astype(np.float64) - cen) @ r).astype(np.float32).astype(np.float64)
+            _, cp, ap, nr, dp = contacts(local)
+            for k in range(len(cp)):
+                deepest[t] = max(deepest[t], dp[k])
+                if best is None or dp[k] > best[3] + 1e-6:
+                    best = (cp[k], ap[k], nr[k], dp[k], t)
+        if best is None or best[4] != 0 or best[3] < 0.1 or deepest[1] > best[3] - 1e-3:
+            continue          # none on T1, too shallow for its normal to hold in float32, or tied with T2's
+        mp, _, wn, _ = _manifold(env)
+        mine = [i for i in range(len(mp)) if np.abs(mp[i] - best[0]).max() < 2e-2]
+        assert len(mine) == 1, trial
+        n = r @ best[2]
+        n /= np.linalg.norm(n)
+        x = r @ best[1] + cen
+        s = np.clip((x - a) @ (b - a) / ((b - a) @ (b - a)), 0.0, 1.0)
+        dist = np.linalg.norm(x - (a + s * (b - a)))
+        ruled, branch, margin = _seam_expected(n, N, Nb, E)
+        if min(margin, abs(dist - 5.0)) < 2e-3:
+            continue                         # too close to a decision boundary for float32
+        changes = np.abs(ruled - n).max() > 1e-2
+        key = (f"within 5 uu: {branch}" if dist < 5.0 else
+               "beyond 5 uu, where the rule would turn it" if changes else "beyond 5 uu, inside the cone")
+        yield dict(trial=trial, pos=pos, rot=q, dist=dist, want=ruled if dist < 5.0 else n, got=wn[mine[0]],
+                   key=key, branch=branch)
+    env.close()
+
+
+@pytest.mark.parametrize("theta_deg", [8, 120])
+def test_manifold_seam_reach_and_sharp_convex_seam_on_a_wedge_mesh(tmp_path, theta_deg):
+    """The internal-edge adjustment's reach and its rejected convex turn
+    (Clip.cuh:91-161), which the arena mesh does not exercise (its contacts
+    off the face normal lie on the contact's own internal edge, and its
+    sharpest convex seam folds 45 degrees): on a wedge mesh (`_wedge_obj`),
+    a car corner or edge pressed 0.2-2 uu into the open edge AB, from above
+    or from below, near the wedge's apex.  The manifold's mesh point is the
+    deepest clip contact; where that lies on T1 within 5 uu of the seam its
+    normal follows the seam's normal cone (`_seam_expected`), and beyond 5
+    uu it keeps the clip normal.  With the seam folded 8 degrees the cone is
+    narrow, so the rule turns most normals both within 5 uu and just beyond
+    (there the reach alone keeps them); folded 120 degrees, a normal turned
+    onto the neighbour's angle would point into T1, and the turn is
+    rejected."""
+    obj = tmp_path / "wedge.obj"
+    apex = _wedge_obj(obj, np.radians(150.0), np.radians(theta_deg))
+    seen = {}
+    for c in wedge_trials(obj, apex, theta_deg, 6000, 150 + theta_deg):
+        np.testing.assert_allclose(c["got"], c["want"], atol=2e-4,
+                                   err_msg=f"trial {c['trial']}: {c['branch']}, {c['dist']:.2f} uu")
+        seen[c["key"]] = seen.get(c["key"], 0) + 1
+    if theta_deg == 8:
+        need = ("within 5 uu: convex: turned onto the neighbour", "beyond 5 uu, where the rule would turn it")
+    else:
+        need = ("within 5 uu: convex: kept (turn rejected)",)
+    for key in need:
+        assert seen.get(key, 0) >= 10, seen
