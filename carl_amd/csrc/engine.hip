@@ -877,6 +877,19 @@ HDI size_t packLdsBytes(int rowLen) { return (size_t)packChunkRows(rowLen) * pac
 
 typedef float F4v __attribute__((ext_vector_type(4)));
 
+// A workgroup barrier that orders LDS accesses only: every thread's LDS reads
+// and writes before it complete before any thread's after it, while its
+// global stores may still be in flight (__syncthreads waits for those too).
+// The packing rounds store a chunk's rows from LDS and then rebuild the LDS
+// with the next chunk: nothing in the workgroup reads the stored rows, so the
+// stores' latency need not be waited for before the rebuild.
+DI void ldsBarrier()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Stores `rows` whole rows (rowLen floats each, row stride `stride` floats in
 // LDS from `lds`) to the contiguous run at dst; 16 bytes per lane and
 // instruction when dst is 16-byte aligned.  The stores are non-temporal: the
@@ -931,14 +944,15 @@ DI void packRowsParts(float* out, int rowLen, int r0, int r1, Keep&& keep, Part&
     const int rowStep = kPackBlock / rowLen, colStep = kPackBlock % rowLen;
     for (int c0 = r0; c0 < r1; c0 += chunk) {
         const int rows = min(chunk, r1 - c0);
+        // keep() depends on the row only: every wave sees the same rows
         const bool mine = lane < rows && keep(c0 + lane);
-        if (q == 0) on[lane] = mine;
-        const int kept = __syncthreads_count(mine);   // every row counted by each of the kRowParts waves
+        const int kept = __popcll(__ballot(mine));
         if (kept == 0) continue;
+        if (q == 0) on[lane] = mine;
         if (mine) part(c0 + lane, q, packLds + lane * stride);
-        __syncthreads();
+        ldsBarrier();
         float* dst = out + (size_t)c0 * rowLen;
-        if (kept == kRowParts * rows) {
+        if (kept == rows) {
             // every row kept: the chunk is one contiguous run
             storeRunFromLds(dst, rowLen, stride, rows, packLds);
         } else {
@@ -951,7 +965,7 @@ DI void packRowsParts(float* out, int rowLen, int r0, int r1, Keep&& keep, Part&
                 if (c >= rowLen) { c -= rowLen; rr++; }
             }
         }
-        __syncthreads();
+        ldsBarrier();
     }
 }
 
@@ -993,7 +1007,7 @@ DI void packRowsGathered(float* out, int rowLen, int i0, int i1, RowOf&& rowOf, 
         const int row = lane < rows ? rowOf(c0 + lane) : 0;
         if (q == 0) rowAt[lane] = row;
         if (lane < rows) part(row, q, packLds + lane * stride);
-        __syncthreads();
+        ldsBarrier();
         const int total = rows * rowLen;
         int rr = t / rowLen, c = t % rowLen;
         for (int e = t; e < total; e += kPackBlock) {
@@ -1002,7 +1016,7 @@ DI void packRowsGathered(float* out, int rowLen, int i0, int i1, RowOf&& rowOf, 
             c += colStep;
             if (c >= rowLen) { c -= rowLen; rr++; }
         }
-        __syncthreads();
+        ldsBarrier();
     }
 }
 
@@ -1124,7 +1138,7 @@ __global__ __launch_bounds__(kPackBlock) void stepEnvKernel(Dev d, StepIO io)
                             ldsB + lane * oStride);
         if (q == 0) listedRow[lane] = (s0 + local) * nC + lane % nC;
     }
-    __syncthreads();
+    ldsBarrier();
     storeRunFromLds(io.tstate + (size_t)s0 * io.stateDim, io.stateDim, sStride, aRows, packLds);
     {
         // the listed rows, each a contiguous run of obsDim floats in tobs
@@ -1134,7 +1148,7 @@ __global__ __launch_bounds__(kPackBlock) void stepEnvKernel(Dev d, StepIO io)
             __builtin_nontemporal_store(ldsB[j * oStride + c], io.tobs + (size_t)listedRow[j] * io.obsDim + c);
         }
     }
-    __syncthreads();
+    ldsBarrier();
     // the rest of the transition state (more cars than one chunk holds) and
     // the transition observations that did not fit
     if (s0 + aRows < s1)
