@@ -359,6 +359,12 @@ DI void carCarPair(const Dev& d, int ia, int ib, int tick)
     Body bA = loadBody(d, ia), bB = loadBody(d, ib);
     const V3 preA = bA.vel, preB = bB.vel;
     solvePair(bA, bB, cts, count);
+    // the bump bookkeeping words, loaded under the integration below (the
+    // bump pass further down reads them; nothing in between writes them)
+    const int cIdxA = d.ci(CARL_CAR_CONTACT_IDX, ia), cIdxB = d.ci(CARL_CAR_CONTACT_IDX, ib);
+    const float coolA = d.cf(CARL_CAR_CONTACT_COOLDOWN, ia), coolB = d.cf(CARL_CAR_CONTACT_COOLDOWN, ib);
+    const bool gndA = d.ci(CARL_CAR_ON_GROUND, ia) != 0, gndB = d.ci(CARL_CAR_ON_GROUND, ib) != 0;
+    const V3 impA = d.cv(CARL_CAR_IMP, ia), impB = d.cv(CARL_CAR_IMP, ib);
     bA.vel = bA.vel + bA.dVel; bA.ang = bA.ang + bA.dAng;
     bB.vel = bB.vel + bB.dVel; bB.ang = bB.ang + bB.dAng;
     bA.pos = bA.pos + bA.pushVel * kDt;
@@ -394,7 +400,7 @@ DI void carCarPair(const Dev& d, int ia, int ib, int tick)
         const int bumper = aB ? ia : ib, victim = aB ? ib : ia;
         const V3 bv = aB ? preA : preB, vv = aB ? preB : preA;
         const V3 delta = (aB ? bB.pos : bA.pos) - (aB ? bA.pos : bB.pos);
-        if (d.ci(CARL_CAR_CONTACT_IDX, bumper) == victim && d.cf(CARL_CAR_CONTACT_COOLDOWN, bumper) > 0.f) continue;
+        if ((aB ? cIdxA : cIdxB) == victim && (aB ? coolA : coolB) > 0.f) continue;
         if (dot(bv, delta) <= 0.f) continue;
         const float speed = len(bv);
         if (speed < 1e-6f) continue;
@@ -402,12 +408,12 @@ DI void carCarPair(const Dev& d, int ia, int ib, int tick)
         const float closing = dot(bv, normalize(delta));
         if (closing <= dot(vv, velDir)) continue;
         if (!frontHit(cts, count, aB, delta, aB ? bA.rot : bB.rot)) continue;
-        const bool grounded = d.ci(CARL_CAR_ON_GROUND, victim) != 0;
+        const bool grounded = aB ? gndB : gndA;
         const float fwdScale = grounded ? bumpCurve(closing, 5.f / 6.f, 1100.f, 1530.f)
                                         : bumpCurve(closing, 5.f / 6.f, 1390.f, 1945.f);
         const V3 up = grounded ? rotate(aB ? bB.rot : bA.rot, kZ) : kZ;
         const V3 imp = velDir * fwdScale + up * bumpCurve(closing, 2.f / 6.f, 278.f, 417.f);
-        d.setv(CARL_CAR_IMP, victim, d.cv(CARL_CAR_IMP, victim) + imp);
+        d.setv(CARL_CAR_IMP, victim, (aB ? impB : impA) + imp);
         d.seti(CARL_CAR_CONTACT_IDX, bumper, victim);
         d.setf(CARL_CAR_CONTACT_COOLDOWN, bumper, kBumpCooldown);
     }
