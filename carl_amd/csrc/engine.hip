@@ -495,14 +495,15 @@ enum ProfWord {
     kProfWords
 };
 
-// Balanced 1v1 launches deal the simulations to the workgroups in units of
-// kUnitSims consecutive simulations: slot s of workgroup b (wave
-// 2 b + s / kWaveUnits) holds one unit, its cars in kUnitCars consecutive
-// lanes and its balls in kUnitSims.  Simulations share nothing, so the deal
-// changes no result; it is made so that the workgroups finish together.  A
-// unit's cars fill whole 128-byte lines of every car field (units of 8
-// simulations left half lines to workgroups on other XCDs, whose L2s then
-// fetched the same lines: the launch read 2.5 times the bytes).
+// Balanced 1v1 and 2v2 launches deal the simulations to the workgroups in
+// units of kUnitCars cars (Deal<Cars>::sims consecutive simulations): slot s
+// of workgroup b (wave 2 b + s / kWaveUnits) holds one unit, its cars in
+// kUnitCars consecutive lanes and its balls in as many lanes as it has
+// simulations.  Simulations share nothing, so the deal changes no result; it
+// is made so that the workgroups finish together.  A unit's cars fill whole
+// 128-byte lines of every car field (1v1 units of 8 simulations left half
+// lines to workgroups on other XCDs, whose L2s then fetched the same lines:
+// the launch read 2.5 times the bytes).
 //
 // The deal needs no pass of its own.  At its last tick every launch files
 // each unit under the class of its cost (dealClass) in an output list: one
@@ -520,11 +521,13 @@ enum ProfWord {
 // list sets rotate: launch L reads set L % 3, files into set (L + 1) % 3
 // (cleared by launch L - 1) and clears the counts of set (L + 2) % 3, which
 // no launch touches again before L + 1.
-constexpr int kUnitSims = 16;   // 32 cars: one 128-byte line of each car field
-constexpr int kBalancedSims = 64;                        // simulations per balanced workgroup
-constexpr int kUnitCars = 2 * kUnitSims;
-constexpr int kUnitSlots = kBalancedSims / kUnitSims;   // units per balanced workgroup
-constexpr int kWaveUnits = kUnitSlots / 2;              // units per wave
+constexpr int kUnitCars = 32;                            // one 128-byte line of each car field
+constexpr int kUnitSlots = 4;                            // units per balanced workgroup
+constexpr int kWaveUnits = kUnitSlots / 2;               // units per wave
+// simulations per unit and per balanced workgroup, by cars per simulation
+// (0: no balanced launch)
+HDI constexpr int dealUnitSims(int cars) { return cars == 2 || cars == 4 ? kUnitCars / cars : 0; }
+HDI constexpr int dealBlockSims(int cars) { return kUnitSlots * dealUnitSims(cars); }
 constexpr int kDealClasses = 32;
 constexpr int kDealSubs = 4;
 constexpr int kDealLists = kDealClasses * kDealSubs;
@@ -571,9 +574,10 @@ DI void tickWindowBody(Dev d0, uint32_t* __restrict__ ws, int screen, int kind, 
                        int tick0, int ticks, int simsPerBlock, SimRange range, WindowMap map,
                        unsigned long long* __restrict__ prof)
 {
-    static_assert(!Balanced || Cars == 2, "balanced launches are 1v1");
-    static_assert(kWindowBlock == 2 * 64 && kWaveUnits * kUnitCars == 64 && kWaveUnits * kUnitSims == kBallOwners,
-                  "a balanced wave holds kWaveUnits units: 64 cars, kBallOwners balls");
+    static_assert(!Balanced || dealUnitSims(Cars) > 0, "balanced launches are 1v1 or 2v2");
+    constexpr int kUnitSims = Balanced ? dealUnitSims(Cars) : 1, kBlockSims = kUnitSlots * kUnitSims;
+    static_assert(kWindowBlock == 2 * 64 && kWaveUnits * kUnitCars == 64 && kWaveUnits * kUnitSims <= kBallOwners,
+                  "a balanced wave holds kWaveUnits units: 64 cars, at most kBallOwners balls");
     // a fixed car count (Cars > 0) lets every per-simulation loop fold
     Dev d = d0;
     if constexpr (Cars > 0) d.nCars = Cars;
@@ -684,7 +688,8 @@ DI void tickWindowBody(Dev d0, uint32_t* __restrict__ ws, int screen, int kind, 
         __syncthreads();
         mark(kStageCarArena);
         if constexpr (Balanced) {
-            ballGroup<Native>(d, tick, slotSim(kBallOwners * wave + (lane & 31)), lane < kBallOwners,
+            constexpr int kWaveSims = kWaveUnits * kUnitSims;
+            ballGroup<Native>(d, tick, slotSim(kWaveSims * wave + lane % kWaveSims), lane < kWaveSims,
                               L.wave[wave].ball, lane);
         } else {
             // the block's simulations split evenly between the waves (a
@@ -699,7 +704,7 @@ DI void tickWindowBody(Dev d0, uint32_t* __restrict__ ws, int screen, int kind, 
         mark(kStageBall);
         if constexpr (Balanced) {
             finishCar(d, slotCar(t));
-            if (t < kBalancedSims) finishBall(d, slotSim(t));
+            if (t < kBlockSims) finishBall(d, slotSim(t));
         } else {
             for (int c = car0 + t; c < carEnd; c += kWindowBlock) finishCar(d, c);
             for (int s = sim0 + t; s < simEnd; s += kWindowBlock) finishBall(d, s);
@@ -709,8 +714,9 @@ DI void tickWindowBody(Dev d0, uint32_t* __restrict__ ws, int screen, int kind, 
         if constexpr (Balanced) {
             int tp = t;
             asm volatile("" : "+v"(tp));
-            const int q = tp / kBalancedSims, j = tp - q * kBalancedSims;
-            boostPadsRange(d, slotSim(j), kPads * q / 2, kPads * (q + 1) / 2);
+            constexpr int kParts = kWindowBlock / kBlockSims;   // pad ranges per simulation
+            const int q = tp / kBlockSims, j = tp - q * kBlockSims;
+            boostPadsRange(d, slotSim(j), kPads * q / kParts, kPads * (q + 1) / kParts);
         } else {
             // boost pads: the workgroup's threads split into kWindowBlock /
             // simsPerBlock parts, each taking a contiguous range of every
@@ -771,7 +777,7 @@ WindowKernel windowKernelFor(int nCars, bool balanced)
 {
     switch (nCars) {
     case 2: return balanced ? tickWindowKernel<2, true> : tickWindowKernel<2, false>;
-    case 4: return tickWindowKernel<4, false>;
+    case 4: return balanced ? tickWindowKernel<4, true> : tickWindowKernel<4, false>;
     case 6: return tickWindowKernel<6, false>;
     default: return tickWindowKernel<0, false>;
     }
@@ -809,7 +815,7 @@ ProfileKernel profileKernelFor(int nCars, bool balanced)
 {
     switch (nCars) {
     case 2: return balanced ? tickWindowProfileKernel<2, true> : tickWindowProfileKernel<2, false>;
-    case 4: return tickWindowProfileKernel<4, false>;
+    case 4: return balanced ? tickWindowProfileKernel<4, true> : tickWindowProfileKernel<4, false>;
     case 6: return tickWindowProfileKernel<6, false>;
     default: return tickWindowProfileKernel<0, false>;
     }
@@ -1792,13 +1798,18 @@ int effectiveWindowSims(const carl_env* e)
     return wsb;
 }
 
-// Whether the next window launch deals its simulations by cost: 1v1 on the
-// mesh arena, one partition, workgroups of kBalancedSims simulations, all
-// of them full.
-bool balancedLaunch(const carl_env* e)
+// Whether a window launch of `ticks` ticks deals its simulations by cost:
+// 1v1 or 2v2 on the mesh arena, one partition, workgroups of dealBlockSims
+// simulations, all of them full, and at least kDealMinTicks ticks.  (A
+// launch of fewer ticks has less tail to even out than the scattered units
+// cost it: 2v2 stepped one tick at a time at 131,072 simulations ran 370 ->
+// 377 us per launch dealt.)
+constexpr int kDealMinTicks = 4;
+bool balancedLaunch(const carl_env* e, int ticks)
 {
-    return e->balance && e->nCars == 2 && !e->native() && e->dealList && std::min(e->tickStreams, e->nSim) == 1
-           && effectiveWindowSims(e) == kBalancedSims && e->nSim % kBalancedSims == 0;
+    const int bs = dealBlockSims(e->nCars);
+    return e->balance && bs > 0 && !e->native() && e->dealList && std::min(e->tickStreams, e->nSim) == 1
+           && effectiveWindowSims(e) == bs && e->nSim % bs == 0 && ticks >= kDealMinTicks;
 }
 
 int launchTicks(carl_env* e, int kind, const void* actions, int n)
@@ -1819,11 +1830,11 @@ int launchTicks(carl_env* e, int kind, const void* actions, int n)
     }
     if (e->windowSims > 0) {
         const int wsb = effectiveWindowSims(e);
-        const bool balanced = balancedLaunch(e);
+        const bool balanced = balancedLaunch(e, n);
         WindowMap map{};
         if (balanced) {
             // the first balanced launch deals the identity
-            const int nU = e->nSim / kUnitSims;
+            const int nU = e->nSim / dealUnitSims(e->nCars);
             const long long l = e->dealLaunches++;
             auto set = [&](long long k, int* base, size_t per) { return base + (size_t)(k % kDealSets) * per; };
             map.inCount = l > 0 ? set(l, e->dealCount, kDealLists) : nullptr;
@@ -2083,9 +2094,9 @@ int carl_env_create(int nSim, int nBlue, int nOrange, int seed, int frameskip, i
     rc = rc ? rc : devAlloc(&e->cactions, nT * 7);
     rc = rc ? rc : devAlloc(&e->ws, (size_t)kWsPlanes * tiledItems(e->nTotal));
     rc = rc ? rc : devAlloc(&e->rowList, nS + 1);
-    if (e->nCars == 2 && nS % kBalancedSims == 0) {
+    if (dealBlockSims(e->nCars) > 0 && nS % dealBlockSims(e->nCars) == 0) {
         rc = rc ? rc : devAlloc(&e->dealCount, (size_t)kDealSets * kDealLists);
-        rc = rc ? rc : devAlloc(&e->dealList, (size_t)kDealSets * kDealClasses * (nS / kUnitSims));
+        rc = rc ? rc : devAlloc(&e->dealList, (size_t)kDealSets * kDealClasses * (nS / dealUnitSims(e->nCars)));
     }
     if (e->native()) rc = rc ? rc : devAlloc(&e->ballScratch, (size_t)kNativeMaxContacts * kNativeSlotWords * nS);
     if (rc) return bail(rc);
@@ -2336,7 +2347,7 @@ int carl_env_get_param(carl_env* e, int p, int* v)
     case CARL_PARAM_TICK_WINDOW_LAUNCH: *v = effectiveWindowSims(e); break;
     case CARL_PARAM_NATIVE_ARENA: *v = e->native(); break;
     case CARL_PARAM_TICK_BALANCE: *v = e->balance; break;
-    case CARL_PARAM_TICK_BALANCED_LAUNCH: *v = balancedLaunch(e); break;
+    case CARL_PARAM_TICK_BALANCED_LAUNCH: *v = balancedLaunch(e, e->frameskip); break;
     default: return fail(CARL_ERR_VALUE, "unknown parameter");
     }
     return CARL_OK;

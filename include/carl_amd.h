@@ -133,16 +133,18 @@ enum {
                                           uses (CARL_PARAM_TICK_WINDOW capped at 128 cars, after the
                                           automatic sizing of small runs; 0: phase kernels); no
                                           reference counterpart */
-    CARL_PARAM_TICK_BALANCE = 16,  /* 1: 1v1 window launches of 64-simulation workgroups deal the
-                                      simulations to the workgroups in units of 16, ordered by the
-                                      contact work each unit did in the balanced launch before, so
-                                      that the workgroups finish together; 0: workgroup b takes
-                                      simulations [64 b, 64 b + 64).  Results are identical; no
-                                      reference counterpart (default 1) */
-    CARL_PARAM_TICK_BALANCED_LAUNCH = 17 /* read-only: 1 when the next window launch is dealt (1v1,
-                                            one partition, 64-simulation workgroups, n_sim a
-                                            multiple of 64, mesh arena, CARL_PARAM_TICK_BALANCE
-                                            on); no reference counterpart */
+    CARL_PARAM_TICK_BALANCE = 16,  /* 1: 1v1 and 2v2 window launches of 64- and 32-simulation
+                                      workgroups deal the simulations to the workgroups in units of
+                                      32 cars (16 or 8 simulations), ordered by the contact work
+                                      each unit did in the balanced launch before, so that the
+                                      workgroups finish together; 0: workgroup b takes simulations
+                                      [S b, S b + S).  Results are identical; no reference
+                                      counterpart (default 1) */
+    CARL_PARAM_TICK_BALANCED_LAUNCH = 17 /* read-only: 1 when the next step's window launch is
+                                            dealt (1v1 or 2v2, one partition, workgroups of 64 or
+                                            32 simulations, n_sim a multiple of that, mesh arena,
+                                            frameskip at least 4, CARL_PARAM_TICK_BALANCE on); no
+                                            reference counterpart */
 };
 
 /* ---- persistent state layout (export / import) ------------------------

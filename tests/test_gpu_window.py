@@ -83,8 +83,16 @@ def test_balanced_deal_1v1(gpu, make_state, reset_every):
     _run_both(8192, 1, 1, 8, 30, make_state, seed=48, streams=1, reset_every=reset_every, balanced=True)
 
 
+def test_balanced_deal_2v2(gpu):
+    """The same for 2v2: units of eight simulations, workgroups of 32, four and
+    eight ticks per step."""
+    _run_both(4096, 2, 2, 8, 20, workloads.clustered_reset_state, seed=49, streams=1, reset_every=4, balanced=True)
+    _run_both(4096, 2, 2, 4, 30, workloads.random_reset_state, seed=50, streams=1, reset_every=1, balanced=True)
+
+
 def test_balanced_launch_conditions(gpu):
-    """The deal runs only for 1v1 in one partition with full workgroups of 64."""
+    """The deal runs only for 1v1 and 2v2 in one partition with full
+    workgroups (64 and 32 simulations)."""
     env = carl_amd.Env(4096, 1, 1, 1, 8, True, False, False)
     env.tick_window, env.tick_streams = 64, 1
     assert env.tick_balance == 1 and env.tick_balanced_launch
@@ -93,10 +101,18 @@ def test_balanced_launch_conditions(gpu):
         assert not env.tick_balanced_launch, attr
         env.tick_window, env.tick_streams, env.tick_balance = 64, 1, 1
         assert env.tick_balanced_launch
-    for n, blue, orange in ((4032 + 8, 1, 1), (2048, 2, 2), (2048, 1, 0)):  # a partial workgroup, 2v2, one car
+    # a partial workgroup, a partial 2v2 workgroup, 3v3, one car
+    for n, blue, orange in ((4032 + 8, 1, 1), (2048 + 16, 2, 2), (2048, 3, 3), (2048, 1, 0)):
         other = carl_amd.Env(n, blue, orange, 1, 8, True, False, False)
         other.tick_window, other.tick_streams = 64, 1
         assert not other.tick_balanced_launch, (n, blue, orange)
+    two = carl_amd.Env(2048, 2, 2, 1, 8, True, False, False)
+    two.tick_window, two.tick_streams = 64, 1            # capped at 128 cars: workgroups of 32
+    assert two.tick_window_launch == 32 and two.tick_balanced_launch
+    for frameskip in (1, 3):                             # too few ticks per launch
+        few = carl_amd.Env(2048, 1, 1, 1, frameskip, True, False, False)
+        few.tick_window, few.tick_streams = 64, 1
+        assert not few.tick_balanced_launch, frameskip
     with pytest.raises(ValueError):
         env.tick_balance = 2
 
