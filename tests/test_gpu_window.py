@@ -90,6 +90,30 @@ def test_balanced_deal_2v2(gpu):
     _run_both(4096, 2, 2, 4, 30, workloads.random_reset_state, seed=50, streams=1, reset_every=1, balanced=True)
 
 
+def test_balanced_deal_bare_ticks(gpu):
+    """Bare tick launches (no packing) are dealt as steps are: a dealt and an
+    undealt environment ticked 8 at a time stay bit-equal, and a launch of 2
+    ticks in between (not dealt) leaves the deal's lists intact for the next
+    dealt launch."""
+    n = 8192
+    rng = np.random.default_rng(51)
+    envs = [carl_amd.Env(n, 1, 1, 5, 8, True, False, False) for _ in range(2)]
+    state = {k: dev(v) for k, v in workloads.clustered_reset_state(rng, n, 2).items()}
+    for env, balance in zip(envs, (1, 0)):
+        env.tick_window, env.tick_streams, env.tick_balance = 64, 1, balance
+        env.apply_reset_state(**state)
+    assert envs[0].tick_balanced_launch and not envs[1].tick_balanced_launch
+    for k in range(12):
+        ticks = 2 if k == 5 else 8
+        actions = dev(workloads.random_continuous_actions(rng, n, 2))
+        for env in envs:
+            env.tick(actions.reshape(-1), 1, ticks)
+        a, b = gpu_state(envs[0]), gpu_state(envs[1])
+        report = describe_mismatch(CAR_NAMES, a[0], b[0]) + describe_mismatch(SIM_NAMES, a[1], b[1])
+        if report:
+            pytest.fail(f"dealt vs undealt after bare launch {k}:\n  " + "\n  ".join(report))
+
+
 def test_balanced_launch_conditions(gpu):
     """The deal runs only for 1v1 and 2v2 in one partition with full
     workgroups (64 and 32 simulations)."""
