@@ -496,7 +496,7 @@ enum ProfWord {
 };
 
 // Balanced 1v1 and 2v2 launches deal the simulations to the workgroups in
-// units of kUnitCars cars (Deal<Cars>::sims consecutive simulations): slot s
+// units of kUnitCars cars (dealUnitSims consecutive simulations): slot s
 // of workgroup b (wave 2 b + s / kWaveUnits) holds one unit, its cars in
 // kUnitCars consecutive lanes and its balls in as many lanes as it has
 // simulations.  Simulations share nothing, so the deal changes no result; it
@@ -554,7 +554,7 @@ DI int dealClass(int cost)
 // list k = kDealSubs c + j of a set holds up to nUnits / kDealSubs units
 // from outList + k nUnits / kDealSubs, its count at outCount[k]
 struct WindowMap {
-    const int* inCount;   // the deal's counts and lists (null: slot s of workgroup b holds unit 8 b + s)
+    const int* inCount;   // the deal's counts and lists (null: slot s of workgroup b holds unit 4 b + s)
     const int* inList;
     int* outCount;        // this launch's filing
     int* outList;
