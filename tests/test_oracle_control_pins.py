@@ -489,6 +489,42 @@ def test_autoroll_on_two_end_wheels_pitches_the_car_level(theta, z, wheels):
     np.testing.assert_allclose(dw, want, atol=2e-6)
 
 
+def _chassis_autoroll_difference(q):
+    """_autoroll_difference for a car high in the air whose arena manifold of
+    the tick before holds one contact of normal +z, as a car lying on the
+    floor leaves it: no wheel touches, so autoroll takes its up direction
+    from that normal."""
+    s = Scene(1, 0)
+    s.place([[0.0, -1500.0, 600.0]], [q], [[0.0, 0.0, 0.0]], [[0.0, 0.0, 0.0]])
+    s.set_fields({("CARL_CAR_MANIFOLD_COUNT", 0): 1, ("CARL_CAR_MANIFOLD_NORMAL_0", 0): 0.0,
+                  ("CARL_CAR_MANIFOLD_NORMAL_1", 0): 0.0, ("CARL_CAR_MANIFOLD_NORMAL_2", 0): 1.0})
+    saved = s.env.export_state()
+    out = []
+    for throttle in (0.0, 0.01):
+        s.env.import_state(*saved)
+        tick_direct(s, direct(throttle=throttle))
+        out.append((s.car_vec("CARL_CAR_VEL", 0), s.car_vec("CARL_CAR_ANG", 0)))
+    s.close()
+    return out[1][0] - out[0][0], out[1][1] - out[0][1]
+
+
+@pytest.mark.parametrize("phi", [0.5, -1.2, 2.0, -2.4, 2.9, -3.1])
+def test_autoroll_from_the_chassis_manifold_saturates_past_a_quarter_roll(phi):
+    """A car rolled by phi about its level nose, touching the floor with its
+    body only: autoroll pushes it down at CAR_AUTOROLL_FORCE and turns it
+    about the nose against the roll, at CAR_AUTOROLL_TORQUE x (1 - cos phi)
+    up to a quarter roll and at the full CAR_AUTOROLL_TORQUE beyond it (on
+    its side or its roof the contact-aligned right axis points against the
+    car's, and the factor stays at 1); the level nose gets no pitch torque."""
+    q = quat_axis_angle((1, 0, 0), phi)
+    dv, dw = _chassis_autoroll_difference(q)
+    nose = rot_matrix(q)[:, 0]
+    np.testing.assert_allclose(dv, [0.0, 0.0, -AUTOROLL_FORCE * DT] + nose * 0.01 * 200.0 / 3.0 * DT, atol=2e-5)
+    factor = 1.0 - max(math.cos(phi), 0.0)
+    want = -math.copysign(1.0, math.sin(phi)) * np.array([1.0, 0.0, 0.0]) * factor * AUTOROLL_TORQUE * DT
+    np.testing.assert_allclose(dw, want, atol=2e-6)
+
+
 def test_no_autoroll_on_four_wheels():
     s = _settled_car()
     saved = s.env.export_state()
