@@ -16,7 +16,9 @@ steps the oracle did not run):
     before);
   * the clustered 3v3 workload at 16,384 simulations (every car within
     500 uu of the ball, at the floor, the walls or the ceiling), compared for
-    its first three steps and again after 100 steps.
+    its first three steps and again after 100 steps;
+  * clustered 2v2 scenes at 32,768 simulations with frameskip 8, whose
+    launches are dealt, after 150 steps.
 """
 import numpy as np
 import pytest
@@ -71,4 +73,21 @@ def test_clustered_3v3_at_walls_and_ceiling(gpu):
     _engine_steps(p, rng, 100)
     p.sync_oracle_from_engine()
     _compared_steps(p, rng, 3, "clustered 3v3 16,384 after 103 steps", synced=True)
+    p.close()
+
+
+@pytest.mark.timeout(900)
+def test_clustered_2v2_dealt_after_150_steps(gpu):
+    """2v2 at 32,768 simulations with frameskip 8 runs dealt launches (32
+    simulations per window workgroup in units of 8); from clustered scenes
+    at the arena's surfaces, 150 steps on the engine, then three compared
+    steps."""
+    rng = np.random.default_rng(32768)
+    n = 32768
+    p = Pair(n, 2, 2, seed=3, frameskip=8)
+    assert p.gpu.tick_window_launch == 32 and p.gpu.tick_balanced_launch
+    p.apply_reset_state(workloads.clustered_reset_state(rng, n, 4))
+    _engine_steps(p, rng, 150)
+    p.sync_oracle_from_engine()
+    _compared_steps(p, rng, 3, "clustered 2v2 32,768 after 150 steps", synced=True)
     p.close()
