@@ -132,6 +132,15 @@ DI bool rayBox(V3 start, V3 dir, V3 center, Q4 rot, float maxDist, float& dist, 
     return true;
 }
 
+// Every wheel ray ends within kWheelReach of the car's box centre: the
+// anchors lie at most 56.1 uu from it, and a ray is at most the longer of the
+// two ray lengths; 4 uu spare cover the rounding of the rays' arithmetic.  A
+// body whose centre is farther than kWheelReach plus its bounding radius
+// meets no wheel ray, so its rays are not cast (each would miss).
+constexpr float kWheelReach = 56.1f + (kFrontRay > kBackRay ? kFrontRay : kBackRay) + 4.f;
+constexpr float kCarRayReach = kWheelReach + 80.f;   // + |kHalf| (76.6) rounded up
+constexpr float kBallRayReach = kWheelReach + kBallRadius;
+
 // rays against the other cars of the simulation, then the ball (after the
 // arena, so only strictly nearer hits replace an arena hit)
 // the wheel rays against one other car's box
@@ -163,7 +172,7 @@ DI void raycastBall(const V3* start, V3 dir, V3 ball, Wheels& w)
 }
 
 // the wheel rays against the simulation's other cars, in car order, then the ball
-DI void raycastBodies(const Dev& d, int car, int sim, const V3* start, V3 dir, Wheels& w)
+DI void raycastBodies(const Dev& d, int car, int sim, V3 cen, const V3* start, V3 dir, Wheels& w)
 {
     const int base = sim * d.nCars;
     const V3 ball = d.sv(CARL_SIM_BALL_POS, sim);
@@ -174,10 +183,10 @@ DI void raycastBodies(const Dev& d, int car, int sim, const V3* start, V3 dir, W
         const int demoed = d.ci(CARL_CAR_DEMOED, oc);
         const V3 ocen = d.cv(CARL_CAR_CEN, oc);
         const Q4 orot = d.cq(CARL_CAR_ROT, oc);
-        if (oc == car || demoed) continue;
+        if (oc == car || demoed || lensq(ocen - cen) > kCarRayReach * kCarRayReach) continue;
         raycastCar(start, dir, ocen, orot, w);
     }
-    raycastBall(start, dir, ball, w);
+    if (!(lensq(ball - cen) > kBallRayReach * kBallRayReach)) raycastBall(start, dir, ball, w);
 }
 
 DI void storeWheelOutputs(const Dev& d, int car, const Wheels& w)
@@ -1326,7 +1335,7 @@ template <int Owners>
 DI int contactFinish(const Dev& d, const ContactLdsT<Owners>& L, int lane, int car, int sim, V3 cen, Q4 rot, Wheels& w)
 {
     return contactFinishWith(L, lane, cen, rot, w,
-                             [&](const V3* start, V3 dir, Wheels& ww) { raycastBodies(d, car, sim, start, dir, ww); });
+                             [&](const V3* start, V3 dir, Wheels& ww) { raycastBodies(d, car, sim, cen, start, dir, ww); });
 }
 
 // --------------------------------------------------------------- solver body

@@ -220,8 +220,9 @@ DI WalkCost contactGroup(const Dev& d, const Handoff& out, int screen, int car, 
     if (ok) {
         if (d.nCars == 2)
             best = contactFinishWith(L, lane, cen, rot, w, [&](const V3* start, V3 dir, Wheels& ww) {
-                if (!odemoed) raycastCar(start, dir, ocen, orot, ww);
-                raycastBall(start, dir, ball, ww);
+                if (!odemoed && !(lensq(ocen - cen) > kCarRayReach * kCarRayReach))
+                    raycastCar(start, dir, ocen, orot, ww);
+                if (!(lensq(ball - cen) > kBallRayReach * kBallRayReach)) raycastBall(start, dir, ball, ww);
             });
         else
             best = contactFinish(d, L, lane, car, car / d.nCars, cen, rot, w);
