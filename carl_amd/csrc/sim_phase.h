@@ -1401,8 +1401,9 @@ constexpr int kMaxCars = 8;
 // tick: disjoint pad ranges of one simulation can run in different threads,
 // in any order, with the same result.  A thread reads every car's boost but
 // uses it only for a car inside one of its own pads, the only case in which
-// it writes that boost.
-template <int MaxCars>
+// it writes that boost.  [P0, P1) bounds the range at compile time (a
+// caller whose range is fixed loads only those pads' cooldowns).
+template <int MaxCars, int P0 = 0, int P1 = kPads>
 DI void boostPadsRangeT(const Dev& d, int s, int p0, int p1)
 {
     const int base = s * d.nCars;
@@ -1425,10 +1426,10 @@ DI void boostPadsRangeT(const Dev& d, int s, int p0, int p1)
     // would wait for its own round trip), those outside the range unused
     float cool[kPads];
 #pragma unroll
-    for (int p = 0; p < kPads; p++) cool[p] = d.sf(CARL_SIM_PAD_COOLDOWN + p, s);
+    for (int p = P0; p < P1; p++) cool[p] = d.sf(CARL_SIM_PAD_COOLDOWN + p, s);
     int changed = 0;
 #pragma unroll
-    for (int p = 0; p < kPads; p++) {
+    for (int p = P0; p < P1; p++) {
         if (p < p0 || p >= p1) continue;
         const float prev = cool[p];
         float cd = prev;
