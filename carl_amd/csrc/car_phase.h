@@ -910,6 +910,10 @@ DI int planeManifold(V3 cen, Q4 rot, ManPt* pts)
     for (int p = 0; p < 4; p++) {
         const V3 nrm = p == 0 ? kZ : (p == 1 ? V3{ 0.f, 0.f, -1.f } : (p == 2 ? kX : V3{ -1.f, 0.f, 0.f }));
         const float off = p == 0 ? 0.f : (p == 1 ? -2044.f : -4096.f);
+        // the box's deepest corner lies within |kHalf| (76.6 uu, taken as 80)
+        // of its centre: a centre farther from the plane than that plus the
+        // contact break gives no point (a wave with no car near a plane skips it)
+        if (dot(nrm, cen) - off >= 80.f + kContactBreak) continue;
         const V3 dir = unrotate(rot, -nrm);
         const V3 carPos{ dir.x >= 0 ? kHalf.x : -kHalf.x, dir.y >= 0 ? kHalf.y : -kHalf.y, dir.z >= 0 ? kHalf.z : -kHalf.z };
         const V3 worldCar = cen + rotate(rot, carPos);
