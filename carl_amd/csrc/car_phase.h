@@ -1588,23 +1588,31 @@ DI void solveManifold(Body& b, const ManPt* pts, int count)
         b.dVel = b.dVel + n.axis * (kCarInvMass * n.applied);
         b.dAng = b.dAng + n.angular * n.applied;
     }
+    // each loop stops at an iteration whose impulses are all exactly zero: it
+    // left every body and row bit for bit as it found them, so each later
+    // iteration would repeat it (the accumulators start at +0 and are never -0)
     for (int it = 0; it < kSolverIters; it++) {
+        bool moved = false;
 #pragma unroll
         for (int i = 0; i < kMaxManifold; i++) {
             if (i >= count) break;
             Row& r = nr[i];
             if (r.rhsPen == 0.f) continue;
             const float imp = pgsLower(r.rhsPen, r.jacInv, rowVel(r, b.pushVel, b.turnVel), r.lower, r.appliedPush);
+            moved |= imp != 0.f;
             b.pushVel = b.pushVel + r.axis * (kCarInvMass * imp);
             b.turnVel = b.turnVel + r.angular * imp;
         }
+        if (!moved) break;
     }
     for (int it = 0; it < kSolverIters; it++) {
+        bool moved = false;
 #pragma unroll
         for (int i = 0; i < kMaxManifold; i++) {
             if (i >= count) break;
             Row& r = nr[i];
             const float imp = pgsLower(r.rhs, r.jacInv, rowVel(r, b.dVel, b.dAng), r.lower, r.applied);
+            moved |= imp != 0.f;
             b.dVel = b.dVel + r.axis * (kCarInvMass * imp);
             b.dAng = b.dAng + r.angular * imp;
         }
@@ -1617,9 +1625,11 @@ DI void solveManifold(Body& b, const ManPt* pts, int count)
             r.lower = -maxImp;
             r.upper = maxImp;
             const float imp = pgsClamp(r.rhs, r.jacInv, rowVel(r, b.dVel, b.dAng), r.lower, r.upper, r.applied);
+            moved |= imp != 0.f;
             b.dVel = b.dVel + r.axis * (kCarInvMass * imp);
             b.dAng = b.dAng + r.angular * imp;
         }
+        if (!moved) break;
     }
 }
 

@@ -219,6 +219,11 @@ DI void pairPush(Body& A, Body& B, const PairRow& r, float imp, bool split)
 }
 
 // 2-body sequential impulses with split penetration recovery (CarCar/Solver.cuh:187-244).
+// An iteration in which every row's impulse is exactly zero leaves the
+// bodies and the rows' accumulated impulses bit for bit as they were (the
+// accumulators start at +0 and are never -0, so adding a zero changes no
+// bit), so every later iteration would repeat it: the loops stop there, with
+// the result of all kSolverIters iterations.
 // The friction rows are built after the split-impulse loop: their inputs (the
 // pre-solve velocities, poses and contact normals) are not changed by it, so
 // the rows are the same, and they need no registers during that loop.
@@ -239,14 +244,17 @@ DI void solvePair(Body& A, Body& B, const PairContact* cts, int count)
         nr[i] = n;
     }
     for (int it = 0; it < kSolverIters; it++) {
+        bool moved = false;
 #pragma unroll
         for (int i = 0; i < kMaxManifold; i++) {
             if (i >= count) break;
             PairRow& r = nr[i];
             const float imp = pgsLower(r.rhsPen, r.jacInv, pairVel(r, A.pushVel, A.turnVel, B.pushVel, B.turnVel), 0.f,
                                        r.appliedPush);
+            moved |= imp != 0.f;
             pairPush(A, B, r, imp, true);
         }
+        if (!moved) break;   // a fixed point: every later iteration would move nothing either
     }
 #pragma unroll
     for (int i = 0; i < kMaxManifold; i++) {
@@ -264,11 +272,13 @@ DI void solvePair(Body& A, Body& B, const PairContact* cts, int count)
         fr[i] = t;
     }
     for (int it = 0; it < kSolverIters; it++) {
+        bool moved = false;
 #pragma unroll
         for (int i = 0; i < kMaxManifold; i++) {
             if (i >= count) break;
             PairRow& r = nr[i];
             const float imp = pgsLower(r.rhs, r.jacInv, pairVel(r, A.dVel, A.dAng, B.dVel, B.dAng), 0.f, r.applied);
+            moved |= imp != 0.f;
             pairPush(A, B, r, imp, false);
         }
 #pragma unroll
@@ -279,8 +289,10 @@ DI void solvePair(Body& A, Body& B, const PairContact* cts, int count)
             PairRow& r = fr[i];
             const float imp = pgsClamp(r.rhs, r.jacInv, pairVel(r, A.dVel, A.dAng, B.dVel, B.dAng), -maxImp, maxImp,
                                        r.applied);
+            moved |= imp != 0.f;
             pairPush(A, B, r, imp, false);
         }
+        if (!moved) break;
     }
 }
 
