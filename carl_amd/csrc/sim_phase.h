@@ -779,24 +779,33 @@ DI void solveBallContacts(BallBody& b, const BallContact* cs, int count, bool wa
     tan = tl > 1e-8f ? tan * rsqrt_(tl) : fallbackTangent(avgN);
     BRow fr = ballRow(tan, avgRel);
     fr.rhs = -bRowVel(fr, b.vel, b.ang) * fr.jacInv;
+    // each loop stops at an iteration whose impulses are all exactly zero (a
+    // fixed point: the accumulators start at +0 and are never -0, so it left
+    // every bit as it found it, and each later iteration would repeat it)
     for (int it = 0; it < kSolverIters; it++) {
+        bool moved = false;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             if (i >= count) break;
             BRow& r = split[i];
             if (r.rhsPen == 0.f) continue;
             const float imp = pgsLower(r.rhsPen, r.jacInv, bRowVel(r, b.pushVel, b.pushAng), 0.f, r.appliedPush);
+            moved |= imp != 0.f;
             ballPush(b, r, imp, true);
         }
+        if (!moved) break;
     }
     for (int it = 0; it < kSolverIters; it++) {
         const float ni = pgsLower(nr.rhs, nr.jacInv, bRowVel(nr, b.dVel, b.dAng), 0.f, nr.applied);
+        bool moved = ni != 0.f;
         ballPush(b, nr, ni, false);
         const float maxImp = kBallFriction * nr.applied;
         if (maxImp > 0.f) {
             const float fi = pgsClamp(fr.rhs, fr.jacInv, bRowVel(fr, b.dVel, b.dAng), -maxImp, maxImp, fr.applied);
+            moved |= fi != 0.f;
             ballPush(b, fr, fi, false);
         }
+        if (!moved) break;
     }
     b.vel = b.vel + b.dVel;
     b.ang = b.ang + b.dAng;
