@@ -1052,7 +1052,9 @@ DI void solveNativeBallContacts(const Dev& d, int sim, BallBody& b, int count, b
     tan = tl > 1e-8f ? tan * rsqrt_(tl) : fallbackTangent(avgN);
     BRow fr = ballRow(tan, avgRel);
     fr.rhs = -bRowVel(fr, b.vel, b.ang) * fr.jacInv;
+    // the loops stop at a fixed point, as in solveBallContacts
     for (int it = 0; it < kSolverIters; it++) {
+        bool moved = false;
         for (int i = 0; i < count; i++) {
             BRow r;
             r.rhsPen = nativeWord(d, sim, i, 7);
@@ -1063,17 +1065,22 @@ DI void solveNativeBallContacts(const Dev& d, int sim, BallBody& b, int count, b
             r.appliedPush = nativeWord(d, sim, i, 8);
             const float imp = pgsLower(r.rhsPen, r.jacInv, bRowVel(r, b.pushVel, b.pushAng), 0.f, r.appliedPush);
             nativeWord(d, sim, i, 8) = r.appliedPush;
+            moved |= imp != 0.f;
             ballPush(b, r, imp, true);
         }
+        if (!moved) break;
     }
     for (int it = 0; it < kSolverIters; it++) {
         const float ni = pgsLower(nr.rhs, nr.jacInv, bRowVel(nr, b.dVel, b.dAng), 0.f, nr.applied);
+        bool moved = ni != 0.f;
         ballPush(b, nr, ni, false);
         const float maxImp = kBallFriction * nr.applied;
         if (maxImp > 0.f) {
             const float fi = pgsClamp(fr.rhs, fr.jacInv, bRowVel(fr, b.dVel, b.dAng), -maxImp, maxImp, fr.applied);
+            moved |= fi != 0.f;
             ballPush(b, fr, fi, false);
         }
+        if (!moved) break;
     }
     b.vel = b.vel + b.dVel;
     b.ang = b.ang + b.dAng;
