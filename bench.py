@@ -290,7 +290,8 @@ def main() -> None:
 
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
-              "(simulations shard across GPUs with no exchange; see DESIGN.md)", file=sys.stderr)
+              "(a multi-GPU run shards the simulations by range, one process per GPU, with no exchange "
+              "inside a step)", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np

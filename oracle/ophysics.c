@@ -6,7 +6,7 @@
  * the same stage order, so cross-car reads see the same values as the
  * reference's kernel sequence.  Per-stage citations are on each function.
  *
- * Ordering choices where the reference is nondeterministic:
+ * Ordering choices where the reference's result depends on thread timing:
  *   - car-triangle SAT hits are recorded in cell-list order (ascending
  *     triangle index) instead of atomicAdd order; at most 32 are kept;
  *   - the global tick counter is reset to 0 before every full reset.
