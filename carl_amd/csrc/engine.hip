@@ -727,7 +727,7 @@ DI void tickWindowBody(Dev d0, uint32_t* __restrict__ ws, int screen, int kind, 
                 else
                     boostPadsRangeT<Cars, kPads / 2, kPads>(d, slotSim(j), kPads / 2, kPads);
             } else {
-                boostPadsRange(d, slotSim(j), kPads * q / kParts, kPads * (q + 1) / kParts);
+                boostPadsSpan(d, slotSim(j), kPads * q / kParts, kPads * (q + 1) / kParts, kParts);
             }
         } else {
             // boost pads: the workgroup's threads split into kWindowBlock /
@@ -740,7 +740,7 @@ DI void tickWindowBody(Dev d0, uint32_t* __restrict__ ws, int screen, int kind, 
             asm volatile("" : "+v"(tp));
             const int parts = kWindowBlock / simsPerBlock, q = tp / simsPerBlock, j = tp - q * simsPerBlock;
             if (q < parts && j < simEnd - sim0)
-                boostPadsRange(d, sim0 + j, kPads * q / parts, kPads * (q + 1) / parts);
+                boostPadsSpan(d, sim0 + j, kPads * q / parts, kPads * (q + 1) / parts, parts);
         }
         __syncthreads();
         mark(kStagePads);

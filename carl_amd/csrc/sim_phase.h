@@ -1491,6 +1491,88 @@ DI void boostPadsRangeT(const Dev& d, int s, int p0, int p1)
         if (changed & (1 << k)) d.setf(CARL_CAR_BOOST, base + k, boost[k]);
 }
 
+// The same for a range of at most Span pads whose bounds vary from lane to
+// lane (the workgroup's pad parts do not line up with its waves): the pads
+// are visited as positions p0 + i, i < Span, so every lane runs the same
+// iterations, with the pads' positions read from the table by index; only
+// the range's cooldowns are loaded (all before the first is used).
+template <int MaxCars, int Span>
+DI void boostPadsSpanT(const Dev& d, int s, int p0, int p1)
+{
+    const int base = s * d.nCars;
+    V3 cp[MaxCars];
+    bool alive[MaxCars];
+    float boost[MaxCars];
+#pragma unroll
+    for (int k = 0; k < MaxCars; k++) {
+        alive[k] = false;
+        cp[k] = kZero;
+        boost[k] = 0.f;
+        if (k < d.nCars) {
+            alive[k] = !d.ci(CARL_CAR_DEMOED, base + k);
+            cp[k] = d.cv(CARL_CAR_POS, base + k);
+            boost[k] = d.cf(CARL_CAR_BOOST, base + k);
+        }
+    }
+    float cool[Span];
+#pragma unroll
+    for (int i = 0; i < Span; i++) cool[i] = d.sf(CARL_SIM_PAD_COOLDOWN + min(p0 + i, kPads - 1), s);
+    int changed = 0;
+#pragma unroll
+    for (int i = 0; i < Span; i++) {
+        const int p = p0 + i;
+        if (p >= p1) break;
+        const float prev = cool[i];
+        float cd = prev;
+        if (cd > 0.f) cd = fmax_(cd - kDt, 0.f);
+        if (cd <= 0.f) {
+            const bool big = p < 6;
+            const float radius = big ? kBigPadRadius : kSmallPadRadius;
+            const float px = kPadPos[p][0], py = kPadPos[p][1], pz = kPadPos[p][2];
+            int locked = -1;
+            float have = 0.f;
+#pragma unroll
+            for (int k = 0; k < MaxCars; k++) {
+                if (k >= d.nCars || !alive[k]) continue;
+                const float dx = cp[k].x - px, dy = cp[k].y - py;
+                if (dx * dx + dy * dy < radius * radius && fabsf(cp[k].z - pz) < kPadHeight) {
+                    locked = k;
+                    have = boost[k];
+                }
+            }
+            if (locked >= 0 && have < kBoostMax) {
+                const float next = fmin_(have + (big ? kBigPadAmount : kSmallPadAmount), kBoostMax);
+                setAt(boost, locked, next);
+                changed |= 1 << locked;
+                cd = big ? kBigPadCooldown : kSmallPadCooldown;
+            }
+        }
+        if (__float_as_uint(cd) != __float_as_uint(prev)) d.ssetf(CARL_SIM_PAD_COOLDOWN + p, s, cd);
+    }
+#pragma unroll
+    for (int k = 0; k < MaxCars; k++)
+        if (changed & (1 << k)) d.setf(CARL_CAR_BOOST, base + k, boost[k]);
+}
+
+// pads [p0, p1) of simulation s, the range at most ceil(kPads / parts) long
+DI void boostPadsSpan(const Dev& d, int s, int p0, int p1, int parts)
+{
+    const int span = (kPads + parts - 1) / parts;
+    if (d.nCars <= 2) {
+        if (span <= 3) boostPadsSpanT<2, 3>(d, s, p0, p1);
+        else if (span <= 9) boostPadsSpanT<2, 9>(d, s, p0, p1);
+        else if (span <= kPads / 2) boostPadsSpanT<2, kPads / 2>(d, s, p0, p1);
+        else boostPadsSpanT<2, kPads>(d, s, p0, p1);
+    } else if (d.nCars <= 4) {
+        if (span <= 3) boostPadsSpanT<4, 3>(d, s, p0, p1);
+        else if (span <= 9) boostPadsSpanT<4, 9>(d, s, p0, p1);
+        else boostPadsSpanT<4, kPads>(d, s, p0, p1);
+    } else {
+        if (span <= 6) boostPadsSpanT<kMaxCars, 6>(d, s, p0, p1);
+        else boostPadsSpanT<kMaxCars, kPads>(d, s, p0, p1);
+    }
+}
+
 DI void boostPadsRange(const Dev& d, int s, int p0, int p1)
 {
     if (d.nCars <= 2) boostPadsRangeT<2>(d, s, p0, p1);

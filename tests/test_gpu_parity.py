@@ -148,6 +148,31 @@ def test_boost_pad_pickups(gpu, n_blue, n_orange):
     p.close()
 
 
+@pytest.mark.parametrize("n_blue,n_orange,window,frameskip", [
+    (1, 0, 128, 2),   # one car per simulation: one range of all 34 pads
+    (1, 1, 64, 2),    # two ranges of 17 (launches too short to be dealt)
+    (1, 1, 32, 2),    # four ranges of 8 or 9
+    (2, 2, 32, 8),    # dealt 2v2 launches: four ranges of 8 or 9
+    (3, 3, 21, 2),    # six ranges of 5 or 6
+])
+def test_boost_pad_ranges_by_workgroup_size(gpu, n_blue, n_orange, window, frameskip):
+    """The window kernel splits each simulation's pads into as many ranges as
+    its workgroup has threads per simulation; cars parked on pads, for every
+    split the workgroup sizes give: pickups and cooldowns against the
+    oracle."""
+    rng = np.random.default_rng(window + 7 * n_blue + n_orange)
+    n, nc = 128, n_blue + n_orange
+    p = Pair(n, n_blue, n_orange, seed=6, frameskip=frameskip)
+    p.gpu.tick_window = window
+    assert p.gpu.tick_window_launch == window
+    p.apply_reset_state(pad_reset_state(rng, n, nc))
+    for step in range(8):
+        p.step_continuous(workloads.random_continuous_actions(rng, n, nc))
+        _assert_clean(p.state_mismatches(), f"{n_blue}v{n_orange} window {window}: state after step {step}")
+        _assert_clean(p.output_mismatches(), f"{n_blue}v{n_orange} window {window}: outputs after step {step}")
+    p.close()
+
+
 def test_dense_geometry_1v1_and_3v3(gpu):
     """Cars and balls in corners, goal mouths, on posts, walls and the ceiling:
     long cell runs, many SAT hits and large ball contact lists."""
