@@ -875,7 +875,9 @@ DI bool triBestContact(const LocalTri& t, const Sat& s, const V3* near, int nNea
     for (int j = 3; j < kMaxPolygon; j++) poly.v[j] = kZero;
     poly.n = 3;
     const int faceAxis = argmax3(vabs(s.minAxis));
-#pragma unroll
+    // a loop, not unrolled: six inlined copies of the clip cost the kernel
+    // code size for no speed
+#pragma unroll 1
     for (int a = 0; a < 3; a++) {
         if (a == faceAxis) continue;
 #pragma unroll

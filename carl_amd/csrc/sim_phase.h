@@ -150,7 +150,7 @@ DI int boxBoxContacts(const Sat& s, const Box& A, const Box& B, PairContact* out
 #pragma unroll
     for (int j = 4; j < kMaxPolygon; j++) poly.v[j] = kZero;
     poly.n = 4;
-#pragma unroll
+#pragma unroll 1   // a loop: the clip's inlined copies would cost code size
     for (int a = 0; a < 3; a++) {
         if (a == faxis || poly.n == 0) continue;
         const V3 side = boxAxis(ref, a);
