@@ -739,8 +739,18 @@ DI void tickWindowBody(Dev d0, uint32_t* __restrict__ ws, int screen, int kind, 
             int tp = t;
             asm volatile("" : "+v"(tp));
             const int parts = kWindowBlock / simsPerBlock, q = tp / simsPerBlock, j = tp - q * simsPerBlock;
-            if (q < parts && j < simEnd - sim0)
+            if (parts == kWindowWaves) {
+                // one range per wave (at most two cars per simulation): fixed
+                // at compile time, as in dealt 1v1 launches
+                if (j < simEnd - sim0) {
+                    if (__builtin_amdgcn_readfirstlane(wave) == 0)
+                        boostPadsRangeT<2, 0, kPads / 2>(d, sim0 + j, 0, kPads / 2);
+                    else
+                        boostPadsRangeT<2, kPads / 2, kPads>(d, sim0 + j, kPads / 2, kPads);
+                }
+            } else if (q < parts && j < simEnd - sim0) {
                 boostPadsSpan(d, sim0 + j, kPads * q / parts, kPads * (q + 1) / parts, parts);
+            }
         }
         __syncthreads();
         mark(kStagePads);
